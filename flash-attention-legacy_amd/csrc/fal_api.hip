@@ -1,0 +1,398 @@
+// C-ABI entry points of libfal_hip.so (declared in include/fal_api.h).
+//
+// This layer replaces the reference's pybind11 binding (csrc/flash_attn_legacy.cpp):
+// it validates shapes, strides and alignment, lays out the caller-provided
+// workspace, fills the kernel parameter blocks and enqueues the kernels on the
+// caller's stream.  It never allocates device memory and never synchronises.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "fal_kernels.h"
+#include "../../include/fal_api.h"
+
+using namespace fal;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return FAL_OK;
+}
+
+bool head_dim_ok(int64_t d) { return d == 32 || d == 64 || d == 96 || d == 128 || d == 256; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// A strided operand: 16-byte aligned base and every used stride a multiple of 8
+// elements, so each 8-element row chunk is one aligned 16-byte access.
+int check_operand(const char* name, const void* p, const int64_t* st, bool use_batch) {
+  if (!p) return fail(FAL_ERR_INVALID, "%s: null pointer", name);
+  if (!st) return fail(FAL_ERR_INVALID, "%s: null strides", name);
+  if (!aligned16(p)) return fail(FAL_ERR_INVALID, "%s: base pointer must be 16-byte aligned", name);
+  for (int i = use_batch ? 0 : 1; i < 3; ++i)
+    if (st[i] % 8 != 0 || st[i] < 0)
+      return fail(FAL_ERR_INVALID, "%s: stride[%d]=%lld must be a non-negative multiple of 8", name, i,
+                  (long long)st[i]);
+  return FAL_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(FAL_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+float scale_log2(float scale) {
+  // |scale| * log2(e); clamped away from 0 so masked scores (-inf) stay -inf.
+  const float a = std::fabs(scale) * kLog2e;
+  return a < 1e-30f ? 1e-30f : a;
+}
+
+bool dims_ok(int64_t x) { return x >= 0 && x <= 0x7fffffff; }
+
+}  // namespace
+
+extern "C" {
+
+const char* fal_last_error(void) { return g_err.c_str(); }
+
+const char* fal_version(void) { return "0.5.0+gfx950"; }
+
+int fal_device_supported(int device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
+            int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
+            const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream) {
+  if (!head_dim_ok(head_dim))
+    return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
+  if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(seqlen_q) || !dims_ok(seqlen_k))
+    return fail(FAL_ERR_INVALID, "invalid sizes");
+  if (heads_q % heads_kv != 0)
+    return fail(FAL_ERR_INVALID, "num_heads_q (%lld) must be divisible by num_heads_kv (%lld)",
+                (long long)heads_q, (long long)heads_kv);
+  int rc;
+  if ((rc = check_operand("q", q, q_strides, true)) || (rc = check_operand("k", k, k_strides, true)) ||
+      (rc = check_operand("v", v, v_strides, true)) || (rc = check_operand("o", o, o_strides, true)))
+    return rc;
+  if (!lse) return fail(FAL_ERR_INVALID, "lse: null pointer");
+  if (batch == 0 || seqlen_q == 0) return ok();
+
+  FwdParams p{};
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(k);
+  p.v = static_cast<const half_t*>(v);
+  p.o = static_cast<half_t*>(o);
+  p.lse = lse;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.l_sb = heads_q * seqlen_q; p.l_sh = seqlen_q; p.l_ss = 1;
+  p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
+  p.Nq = (int)seqlen_q; p.Nk = (int)seqlen_k;
+  p.scale_log2 = scale_log2(softmax_scale);
+  p.negate_q = softmax_scale < 0.f;
+  const int bm = fwd_block_m((int)head_dim);
+  p.n_qtiles = cdiv((int)seqlen_q, bm);
+  const int64_t nblocks = (int64_t)p.n_qtiles * batch * heads_q;
+  if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
+  return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks),
+                                  static_cast<hipStream_t>(stream)),
+                       "fal_fwd");
+}
+
+size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q, int64_t head_dim) {
+  (void)max_seqlen_q;
+  const int bm = fwd_block_m(head_dim_ok(head_dim) ? (int)head_dim : 128);
+  const int64_t cap = (total_q + bm - 1) / bm + num_seqs;
+  return align256((size_t)cap * sizeof(int2));
+}
+
+int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* lse,
+                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t total_q,
+                   int64_t total_k, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_q,
+                   int64_t max_seqlen_k, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* o_strides, float softmax_scale, int is_causal,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  (void)max_seqlen_k;
+  if (!head_dim_ok(head_dim))
+    return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
+  if (num_seqs < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(total_q) || !dims_ok(total_k) ||
+      max_seqlen_q < 0)
+    return fail(FAL_ERR_INVALID, "invalid sizes");
+  if (heads_q % heads_kv != 0)
+    return fail(FAL_ERR_INVALID, "H_q (%lld) must be divisible by H_kv (%lld)", (long long)heads_q,
+                (long long)heads_kv);
+  if (!cu_seqlens_q || !cu_seqlens_k) return fail(FAL_ERR_INVALID, "cu_seqlens: null pointer");
+  int rc;
+  if ((rc = check_operand("q", q, q_strides, false)) || (rc = check_operand("k", k, k_strides, false)) ||
+      (rc = check_operand("v", v, v_strides, false)) || (rc = check_operand("o", o, o_strides, false)))
+    return rc;
+  if (!lse) return fail(FAL_ERR_INVALID, "lse: null pointer");
+  const size_t need = fal_fwd_varlen_workspace_size(num_seqs, total_q, max_seqlen_q, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  if (num_seqs == 0 || total_q == 0) return ok();
+
+  const int bm = fwd_block_m((int)head_dim);
+  const int cap = (int)((total_q + bm - 1) / bm + num_seqs);
+  int2* work = static_cast<int2*>(workspace);
+  int nb = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
+  nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, bm, nb, is_causal ? 1 : 0, work, cap, st);
+  if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
+
+  FwdParams p{};
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(k);
+  p.v = static_cast<const half_t*>(v);
+  p.o = static_cast<half_t*>(o);
+  p.lse = lse;
+  p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.l_sb = 0; p.l_sh = 1; p.l_ss = heads_q;
+  p.B = 1; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
+  p.scale_log2 = scale_log2(softmax_scale);
+  p.negate_q = softmax_scale < 0.f;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.work = work;
+  return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_q), st),
+                       "fal_fwd_varlen");
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------
+size_t fal_bwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t head_dim) {
+  const size_t rows = (size_t)batch * heads_q * seqlen_q;
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+}
+
+static int fill_bwd_common(BwdParams& p, const void* dout, const void* q, const void* k, const void* v,
+                           const void* o, const float* lse, void* dq, void* dk, void* dv,
+                           const int64_t* do_s, const int64_t* q_s, const int64_t* k_s, const int64_t* v_s,
+                           const int64_t* o_s, const int64_t* dq_s, const int64_t* dk_s, const int64_t* dv_s,
+                           bool batched) {
+  int rc;
+  if ((rc = check_operand("dout", dout, do_s, batched)) || (rc = check_operand("q", q, q_s, batched)) ||
+      (rc = check_operand("k", k, k_s, batched)) || (rc = check_operand("v", v, v_s, batched)) ||
+      (rc = check_operand("o", o, o_s, batched)) || (rc = check_operand("dq", dq, dq_s, batched)) ||
+      (rc = check_operand("dk", dk, dk_s, batched)) || (rc = check_operand("dv", dv, dv_s, batched)))
+    return rc;
+  if (!lse) return fail(FAL_ERR_INVALID, "lse: null pointer");
+  p.dout = static_cast<const half_t*>(dout);
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(k);
+  p.v = static_cast<const half_t*>(v);
+  p.o = static_cast<const half_t*>(o);
+  p.lse = lse;
+  p.dq = static_cast<half_t*>(dq);
+  p.dk = static_cast<half_t*>(dk);
+  p.dv = static_cast<half_t*>(dv);
+  p.do_sb = batched ? do_s[0] : 0; p.do_sh = do_s[1]; p.do_ss = do_s[2];
+  p.q_sb = batched ? q_s[0] : 0; p.q_sh = q_s[1]; p.q_ss = q_s[2];
+  p.k_sb = batched ? k_s[0] : 0; p.k_sh = k_s[1]; p.k_ss = k_s[2];
+  p.v_sb = batched ? v_s[0] : 0; p.v_sh = v_s[1]; p.v_ss = v_s[2];
+  p.o_sb = batched ? o_s[0] : 0; p.o_sh = o_s[1]; p.o_ss = o_s[2];
+  p.dq_sb = batched ? dq_s[0] : 0; p.dq_sh = dq_s[1]; p.dq_ss = dq_s[2];
+  p.dk_sb = batched ? dk_s[0] : 0; p.dk_sh = dk_s[1]; p.dk_ss = dk_s[2];
+  p.dv_sb = batched ? dv_s[0] : 0; p.dv_sh = dv_s[1]; p.dv_ss = dv_s[2];
+  return FAL_OK;
+}
+
+static int run_bwd(BwdParams& p, int d, int causal, dim3 grid, bool batched, hipStream_t st) {
+  hipError_t e = launch_bwd_pre(p, d, batched ? 1 : 0, st);
+  if (e != hipSuccess) return launch_status(e, "bwd preprocess");
+  if (grid.x > 0 && grid.y > 0) {
+    e = launch_bwd(p, d, causal, grid, st);
+    if (e != hipSuccess) return launch_status(e, "bwd main");
+  }
+  e = launch_bwd_post(p, d, st);
+  return launch_status(e, "bwd dq cast");
+}
+
+int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+            void* dq, void* dk, void* dv, int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t seqlen_q,
+            int64_t seqlen_k, int64_t head_dim, const int64_t* do_strides, const int64_t* q_strides,
+            const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+            const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+            float softmax_scale, int is_causal, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!head_dim_ok(head_dim))
+    return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
+  if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(seqlen_q) || !dims_ok(seqlen_k))
+    return fail(FAL_ERR_INVALID, "invalid sizes");
+  if (heads_q % heads_kv != 0) return fail(FAL_ERR_INVALID, "H_q must be divisible by H_kv for GQA");
+  BwdParams p{};
+  int rc = fill_bwd_common(p, dout, q, k, v, o, lse, dq, dk, dv, do_strides, q_strides, k_strides, v_strides,
+                           o_strides, dq_strides, dk_strides, dv_strides, true);
+  if (rc) return rc;
+  const size_t need = fal_bwd_workspace_size(batch, heads_q, seqlen_q, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  if (batch == 0 || seqlen_k == 0 && seqlen_q == 0) return ok();
+  const size_t rows = (size_t)batch * heads_q * seqlen_q;
+  p.dq_acc = static_cast<float*>(workspace);
+  p.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * head_dim * sizeof(float)));
+  p.dqa_sb = heads_q * seqlen_q * head_dim; p.dqa_sh = seqlen_q * head_dim; p.dqa_ss = head_dim;
+  p.l_sb = heads_q * seqlen_q; p.l_sh = seqlen_q; p.l_ss = 1;
+  p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
+  p.Nq = (int)seqlen_q; p.Nk = (int)seqlen_k;
+  p.scale = softmax_scale;
+  p.scale_log2 = softmax_scale * kLog2e;
+  const int bn = bwd_block_n((int)head_dim);
+  p.n_ktiles = cdiv((int)seqlen_k, bn);
+  const int64_t nblocks = (int64_t)p.n_ktiles * batch * heads_kv;
+  if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
+  return run_bwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), true, static_cast<hipStream_t>(stream));
+}
+
+size_t fal_bwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q,
+                                     int64_t head_dim) {
+  const size_t rows = (size_t)total_q * heads_q;
+  const int bn = bwd_block_n(head_dim_ok(head_dim) ? (int)head_dim : 128);
+  const size_t cap = (size_t)((total_k + bn - 1) / bn + num_seqs);
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) + align256(cap * sizeof(int2));
+}
+
+int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+                   void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                   int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,
+                   int64_t head_dim, int64_t max_seqlen_q, int64_t max_seqlen_k, const int64_t* do_strides,
+                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, const int64_t* dq_strides, const int64_t* dk_strides,
+                   const int64_t* dv_strides, float softmax_scale, int is_causal, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  (void)max_seqlen_q;
+  if (!head_dim_ok(head_dim))
+    return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
+  if (num_seqs < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(total_q) || !dims_ok(total_k) ||
+      max_seqlen_k < 0)
+    return fail(FAL_ERR_INVALID, "invalid sizes");
+  if (heads_q % heads_kv != 0) return fail(FAL_ERR_INVALID, "H_q must be divisible by H_kv for GQA");
+  if (!cu_seqlens_q || !cu_seqlens_k) return fail(FAL_ERR_INVALID, "cu_seqlens: null pointer");
+  BwdParams p{};
+  int rc = fill_bwd_common(p, dout, q, k, v, o, lse, dq, dk, dv, do_strides, q_strides, k_strides, v_strides,
+                           o_strides, dq_strides, dk_strides, dv_strides, false);
+  if (rc) return rc;
+  const size_t need = fal_bwd_varlen_workspace_size(num_seqs, total_q, total_k, heads_q, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (total_q == 0 && total_k == 0) return ok();
+  const size_t rows = (size_t)total_q * heads_q;
+  char* ws = static_cast<char*>(workspace);
+  p.dq_acc = reinterpret_cast<float*>(ws);
+  ws += align256(rows * head_dim * sizeof(float));
+  p.delta = reinterpret_cast<float*>(ws);
+  ws += align256(rows * sizeof(float));
+  int2* work = reinterpret_cast<int2*>(ws);
+  p.dqa_sb = 0; p.dqa_sh = head_dim; p.dqa_ss = heads_q * head_dim;
+  p.l_sb = 0; p.l_sh = 1; p.l_ss = heads_q;
+  p.B = 1; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
+  p.total_q = (int)total_q;
+  p.scale = softmax_scale;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.work = work;
+  const int bn = bwd_block_n((int)head_dim);
+  const int cap = (int)((total_k + bn - 1) / bn + num_seqs);
+  int nb = cdiv((int)(max_seqlen_k > 0 ? max_seqlen_k : 1), bn);
+  nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
+  // Every key row of every segment is covered by exactly one work item, which writes
+  // its dK/dV rows (zeros when the segment has no query rows).  Rows outside all
+  // segments are not written; the caller pre-zeroes dk/dv if it needs them defined.
+  hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, bn, nb, 0, work, cap, st);
+  if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen schedule");
+  return run_bwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_kv), false, st);
+}
+
+// ---------------------------------------------------------------------------
+// Decode
+// ---------------------------------------------------------------------------
+size_t fal_decode_workspace_size(int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t max_seqlen_k,
+                                 int64_t head_dim) {
+  const int d = head_dim_ok(head_dim) ? (int)head_dim : 128;
+  const int chunk = decode_chunk(d, (int)batch, (int)(heads_kv > 0 ? heads_kv : 1),
+                                 (int)(max_seqlen_k > 0 ? max_seqlen_k : 1));
+  const int64_t ms = (max_seqlen_k + chunk - 1) / chunk < 1 ? 1 : (max_seqlen_k + chunk - 1) / chunk;
+  const size_t parts = (size_t)batch * heads_q * ms;
+  return align256(parts * head_dim * sizeof(float)) + align256(parts * sizeof(float));
+}
+
+int fal_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
+               const float* mask_bias, int64_t mask_stride, void* o, float* lse, int64_t batch, int64_t heads_q,
+               int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_k, const int64_t* q_strides,
+               const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+               float softmax_scale, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!head_dim_ok(head_dim))
+    return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
+  if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(max_seqlen_k))
+    return fail(FAL_ERR_INVALID, "invalid sizes");
+  if (heads_q % heads_kv != 0) return fail(FAL_ERR_INVALID, "H_q must be divisible by H_kv");
+  if (heads_q / heads_kv > 32)
+    return fail(FAL_ERR_UNSUPPORTED, "decode supports at most 32 query heads per KV head, got %lld",
+                (long long)(heads_q / heads_kv));
+  if (!cache_seqlens) return fail(FAL_ERR_INVALID, "cache_seqlens: null pointer");
+  int rc;
+  if ((rc = check_operand("q", q, q_strides, true)) || (rc = check_operand("k_cache", k_cache, k_strides, true)) ||
+      (rc = check_operand("v_cache", v_cache, v_strides, true)) || (rc = check_operand("o", o, o_strides, true)))
+    return rc;
+  const size_t need = fal_decode_workspace_size(batch, heads_q, heads_kv, max_seqlen_k, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  if (batch == 0) return ok();
+  DecodeParams p{};
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(k_cache);
+  p.v = static_cast<const half_t*>(v_cache);
+  p.seqlens = cache_seqlens;
+  p.bias = mask_bias;
+  p.bias_sb = mask_stride;
+  p.o = static_cast<half_t*>(o);
+  p.lse = lse;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1];
+  p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
+  p.chunk = decode_chunk((int)head_dim, (int)batch, (int)heads_kv, (int)(max_seqlen_k > 0 ? max_seqlen_k : 1));
+  p.max_splits = cdiv((int)(max_seqlen_k > 0 ? max_seqlen_k : 1), p.chunk);
+  const size_t parts = (size_t)batch * heads_q * p.max_splits;
+  p.part_o = static_cast<float*>(workspace);
+  p.part_m = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(parts * head_dim * sizeof(float)));
+  p.scale_log2 = scale_log2(softmax_scale);
+  p.negate_q = softmax_scale < 0.f;
+  if (batch > 65535) return fail(FAL_ERR_INVALID, "batch too large for one launch");
+  return launch_status(launch_decode(p, (int)head_dim, static_cast<hipStream_t>(stream)), "fal_decode");
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// Kernel parameter blocks and launcher declarations shared by the kernel
+// translation units and the C-ABI layer.  Strides are in elements and 64-bit
+// (the reference's int32 strides, csrc/include/flash_attn_common.h:25-147,
+// overflow above 2^31 elements); the last dimension is always unit-stride.
+#pragma once
+
+#include "fal_common.h"
+
+namespace fal {
+
+// Forward.  Batched mode (cu_q == nullptr): tensors are [B, H, N, d] addressed
+// by (b, h, n) strides.  Varlen mode: b is 0, the "seq" stride is the token
+// stride of the packed [total, H, d] tensor and cu_q/cu_k give the segments;
+// `work` is the (sequence, query-tile) list built by varlen_schedule_kernel.
+struct FwdParams {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  half_t* o;
+  float* lse;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int64_t l_sb, l_sh, l_ss;
+  int B, Hq, Hkv, Nq, Nk;
+  int n_qtiles;
+  float scale_log2;   // |softmax_scale| * log2(e)
+  int negate_q;       // softmax_scale < 0
+  const int* cu_q;
+  const int* cu_k;
+  const int2* work;
+};
+
+// Backward.  Same addressing as FwdParams, plus dO (do_*), the fp32 dQ
+// accumulator (dqa_*, same layout as Q but float), dK/dV outputs and the
+// per-row delta = rowsum(dO * O) (same layout as lse).
+struct BwdParams {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  const half_t* o;
+  const half_t* dout;
+  const float* lse;
+  float* delta;
+  float* dq_acc;
+  half_t* dq;
+  half_t* dk;
+  half_t* dv;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int64_t do_sb, do_sh, do_ss;
+  int64_t l_sb, l_sh, l_ss;
+  int64_t dqa_sb, dqa_sh, dqa_ss;
+  int64_t dq_sb, dq_sh, dq_ss;
+  int64_t dk_sb, dk_sh, dk_ss;
+  int64_t dv_sb, dv_sh, dv_ss;
+  int B, Hq, Hkv, Nq, Nk;
+  int n_ktiles;
+  float scale;        // softmax_scale (signed)
+  float scale_log2;   // softmax_scale * log2(e) (signed)
+  const int* cu_q;
+  const int* cu_k;
+  const int2* work;   // (sequence, kv-tile) list in varlen mode
+  int total_q;        // varlen: rows of the packed Q (row-wise kernels)
+};
+
+// KV-cache decode (one query token per sequence).
+struct DecodeParams {
+  const half_t* q;          // [B, Hq, d] via (q_sb, q_sh)
+  const half_t* k;          // cache rows via (k_sb, k_ss, k_sh)
+  const half_t* v;
+  const int* seqlens;       // [B] valid cache rows
+  const float* bias;        // optional additive mask [B, bias_sb]
+  half_t* o;                // [B, Hq, d] via (o_sb, o_sh)
+  float* lse;               // optional [B, Hq] natural-log LSE
+  float* part_o;            // [B, Hq, max_splits, d] fp32 partial outputs
+  float* part_m;            // [B, Hq, max_splits] partial log2-domain LSE
+  int64_t q_sb, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t o_sb, o_sh;
+  int64_t bias_sb;
+  int B, Hq, Hkv, max_splits, chunk;
+  float scale_log2;
+  int negate_q;
+};
+
+hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
+int fwd_block_m(int d);
+hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int tile, int nbuckets, int descending,
+                                  int2* work, int capacity, hipStream_t st);
+
+int bwd_block_n(int d);
+hipError_t launch_bwd(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
+hipError_t launch_bwd_pre(const BwdParams& p, int d, int rows_batched, hipStream_t st);
+hipError_t launch_bwd_post(const BwdParams& p, int d, hipStream_t st);
+
+int decode_chunk(int d, int B, int Hkv, int max_seqlen);
+hipError_t launch_decode(const DecodeParams& p, int d, hipStream_t st);
+
+}  // namespace fal

@@ -1,0 +1,303 @@
+"""ctypes binding of libfal_hip.so -- the drop-in for the reference's compiled
+extension module ``flash_attn_legacy_cuda`` (csrc/flash_attn_legacy.cpp:294-310).
+
+It exposes the reference's three functions with the same arguments, outputs and
+error behaviour (``RuntimeError`` with the library's message):
+
+* ``forward(Q, K, V, softmax_scale, is_causal=False) -> [O, L]``
+* ``forward_varlen(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+  softmax_scale, is_causal=False) -> [O, L]``
+* ``backward(dO, Q, K, V, O, L, softmax_scale, is_causal=False) -> [dQ, dK, dV]``
+
+plus two entry points the reference does not have:
+
+* ``backward_varlen(...)`` -- one launch for all packed sequences;
+* ``decode(q, k_cache, v_cache, cache_seqlens, softmax_scale, ...)`` -- split-K
+  KV-cache decode.
+
+Outputs and workspaces are allocated here with torch on the input's device; the
+library itself never allocates.  Work is enqueued on the current torch stream.
+There is no fallback: if the shared library is missing, importing this module
+raises ``ImportError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Optional
+
+import torch
+
+_LIB_NAME = "libfal_hip.so"
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+_INT = ctypes.c_int
+_SZ = ctypes.c_size_t
+_STR = ctypes.POINTER(ctypes.c_int64)
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(_LIB_PATH):
+        raise ImportError(
+            f"flash_attn_legacy HIP library not found at {_LIB_PATH}. "
+            "Build it with: python flash-attention-legacy_amd/build.py"
+        )
+    lib = ctypes.CDLL(_LIB_PATH)
+    sig = {
+        "fal_last_error": (ctypes.c_char_p, []),
+        "fal_version": (ctypes.c_char_p, []),
+        "fal_device_supported": (_INT, [_INT]),
+        "fal_fwd": (_INT, [_VP] * 5 + [_I64] * 6 + [_STR] * 4 + [_F32, _INT, _VP]),
+        "fal_fwd_varlen_workspace_size": (_SZ, [_I64] * 4),
+        "fal_fwd_varlen": (_INT, [_VP] * 7 + [_I64] * 8 + [_STR] * 4 + [_F32, _INT, _VP, _SZ, _VP]),
+        "fal_bwd_workspace_size": (_SZ, [_I64] * 4),
+        "fal_bwd": (_INT, [_VP] * 9 + [_I64] * 6 + [_STR] * 8 + [_F32, _INT, _VP, _SZ, _VP]),
+        "fal_bwd_varlen_workspace_size": (_SZ, [_I64] * 5),
+        "fal_bwd_varlen": (_INT, [_VP] * 11 + [_I64] * 8 + [_STR] * 8 + [_F32, _INT, _VP, _SZ, _VP]),
+        "fal_decode_workspace_size": (_SZ, [_I64] * 5),
+        "fal_decode": (_INT, [_VP] * 5 + [_I64, _VP, _VP] + [_I64] * 5 + [_STR] * 4 + [_F32, _VP, _SZ, _VP]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = _load()
+
+# Exported names, for introspection and tests.
+SYMBOLS = (
+    "fal_last_error", "fal_version", "fal_device_supported",
+    "fal_fwd", "fal_fwd_varlen_workspace_size", "fal_fwd_varlen",
+    "fal_bwd_workspace_size", "fal_bwd", "fal_bwd_varlen_workspace_size", "fal_bwd_varlen",
+    "fal_decode_workspace_size", "fal_decode",
+)
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def version() -> str:
+    return _lib.fal_version().decode()
+
+
+def device_supported(device: int = 0) -> bool:
+    return bool(_lib.fal_device_supported(int(device)))
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(_lib.fal_last_error().decode() or f"flash_attn_legacy error {rc}")
+
+
+def _strides(t: torch.Tensor, dims=(0, 1, 2)):
+    s = t.stride()
+    return (ctypes.c_int64 * 3)(*[s[i] if i is not None else 0 for i in dims])
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _usable(t: torch.Tensor) -> torch.Tensor:
+    """Keep strided views the kernels can address directly (unit last stride, other
+    strides multiples of 8 elements, 16-byte aligned base); copy anything else."""
+    if t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:-1]):
+        return t
+    return t.contiguous()
+
+
+def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def _check_half_cuda(name: str, t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be on CUDA")
+    if t.dtype != torch.float16:
+        raise RuntimeError(f"{name} must be float16")
+
+
+# ---------------------------------------------------------------------------
+# Reference-compatible entry points
+# ---------------------------------------------------------------------------
+
+def forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, softmax_scale: float,
+            is_causal: bool = False) -> List[torch.Tensor]:
+    """[O, L] for Q [B,Hq,N,d], K/V [B,Hkv,Nk,d]; L is [B,Hq,N] fp32 natural-log LSE.
+    Checks of ``flash_attn_forward`` (csrc/flash_attn_legacy.cpp:48-60)."""
+    _check_half_cuda("Q", Q)
+    if Q.dim() != 4:
+        raise RuntimeError("Q must be [B, H_q, N, d]")
+    if K.dim() != 4 or V.dim() != 4:
+        raise RuntimeError("K,V must be 4D")
+    _check_half_cuda("K", K)
+    _check_half_cuda("V", V)
+    B, Hq, N, d = Q.shape
+    Hkv, Nk = K.shape[1], K.shape[2]
+    if K.shape[0] != B or K.shape[3] != d:
+        raise RuntimeError("K shape mismatch")
+    if tuple(V.shape) != (B, Hkv, Nk, d):
+        raise RuntimeError("V shape mismatch")
+    Q, K, V = _usable(Q), _usable(K), _usable(V)
+    O = torch.empty((B, Hq, N, d), dtype=torch.float16, device=Q.device)
+    L = torch.empty((B, Hq, N), dtype=torch.float32, device=Q.device)
+    with torch.cuda.device(Q.device):
+        _check(_lib.fal_fwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), B, Hq, Hkv, N, Nk, d,
+                            _strides(Q), _strides(K), _strides(V), _strides(O),
+                            float(softmax_scale), int(bool(is_causal)), _stream(Q.device)))
+    return [O, L]
+
+
+def forward_varlen(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int,
+                   softmax_scale: float, is_causal: bool = False) -> List[torch.Tensor]:
+    """[O, L] for packed Q [total_q,Hq,d], K/V [total_k,Hkv,d]; L is [total_q,Hq].
+    Checks of ``flash_attn_forward_varlen`` (csrc/flash_attn_legacy.cpp:201-217).
+    The (sequence, tile) schedule is built on the device: no host synchronisation."""
+    _check_half_cuda("Q", Q)
+    if Q.dim() != 3:
+        raise RuntimeError("Q must be [total_q, H_q, d]")
+    if K.dim() != 3 or V.dim() != 3:
+        raise RuntimeError("K,V must be 3D")
+    if cu_seqlens_q.dtype != torch.int32:
+        raise RuntimeError("cu_seqlens_q must be int32")
+    if cu_seqlens_k.dtype != torch.int32:
+        raise RuntimeError("cu_seqlens_k must be int32")
+    total_q, Hq, d = Q.shape
+    total_k, Hkv = K.shape[0], K.shape[1]
+    num_seqs = cu_seqlens_q.shape[0] - 1
+    if K.shape[2] != d or V.shape[2] != d:
+        raise RuntimeError("K,V head_dim mismatch")
+    if V.shape[1] != Hkv:
+        raise RuntimeError("V num_heads mismatch")
+    if cu_seqlens_k.shape[0] != num_seqs + 1:
+        raise RuntimeError("cu_seqlens_k length mismatch")
+    Q, K, V = _usable(Q), _usable(K), _usable(V)
+    cu_q = cu_seqlens_q.to(Q.device).contiguous()
+    cu_k = cu_seqlens_k.to(Q.device).contiguous()
+    O = torch.empty((total_q, Hq, d), dtype=torch.float16, device=Q.device)
+    L = torch.empty((total_q, Hq), dtype=torch.float32, device=Q.device)
+    ws = _workspace(_lib.fal_fwd_varlen_workspace_size(num_seqs, total_q, int(max_seqlen_q), d), Q.device)
+    with torch.cuda.device(Q.device):
+        _check(_lib.fal_fwd_varlen(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(cu_q), _ptr(cu_k),
+                                   num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
+                                   _strides(Q, (None, 1, 0)), _strides(K, (None, 1, 0)),
+                                   _strides(V, (None, 1, 0)), _strides(O, (None, 1, 0)),
+                                   float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(),
+                                   _stream(Q.device)))
+    return [O, L]
+
+
+def backward(dO, Q, K, V, O, L, softmax_scale: float, is_causal: bool = False) -> List[torch.Tensor]:
+    """[dQ, dK, dV] from the saved forward (O, L).  Checks of ``flash_attn_backward``
+    (csrc/flash_attn_legacy.cpp:115-120); dQ has Q's shape, dK/dV have K/V's."""
+    if not (Q.is_cuda and Q.dtype == torch.float16):
+        raise RuntimeError("Q must be CUDA float16")
+    if dO.shape != Q.shape:
+        raise RuntimeError("dO shape must match Q")
+    B, Hq, N, d = Q.shape
+    Hkv, Nk = K.shape[1], K.shape[2]
+    if Hq % Hkv != 0:
+        raise RuntimeError("H_q must be divisible by H_kv for GQA")
+    for name, t in (("dO", dO), ("K", K), ("V", V), ("O", O)):
+        _check_half_cuda(name, t)
+    dO, Q, K, V, O = (_usable(t) for t in (dO, Q, K, V, O))
+    L = L.contiguous()
+    dQ = torch.empty((B, Hq, N, d), dtype=torch.float16, device=Q.device)
+    dK = torch.empty((B, Hkv, Nk, d), dtype=torch.float16, device=Q.device)
+    dV = torch.empty((B, Hkv, Nk, d), dtype=torch.float16, device=Q.device)
+    ws = _workspace(_lib.fal_bwd_workspace_size(B, Hq, N, d), Q.device)
+    with torch.cuda.device(Q.device):
+        _check(_lib.fal_bwd(_ptr(dO), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(dQ), _ptr(dK), _ptr(dV),
+                            B, Hq, Hkv, N, Nk, d,
+                            _strides(dO), _strides(Q), _strides(K), _strides(V), _strides(O),
+                            _strides(dQ), _strides(dK), _strides(dV),
+                            float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(),
+                            _stream(Q.device)))
+    return [dQ, dK, dV]
+
+
+# ---------------------------------------------------------------------------
+# Entry points without a reference counterpart
+# ---------------------------------------------------------------------------
+
+def backward_varlen(dO, Q, K, V, O, L, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_seqlen_k: int,
+                    softmax_scale: float, is_causal: bool = False) -> List[torch.Tensor]:
+    """[dQ, dK, dV] for packed sequences in one launch.  Same results as the reference's
+    per-sequence loop (flash_attn_legacy/flash_attn.py:133-157): dK/dV rows outside every
+    segment are zero."""
+    if not (Q.is_cuda and Q.dtype == torch.float16):
+        raise RuntimeError("Q must be CUDA float16")
+    if dO.shape != Q.shape:
+        raise RuntimeError("dO shape must match Q")
+    total_q, Hq, d = Q.shape
+    total_k, Hkv = K.shape[0], K.shape[1]
+    num_seqs = cu_seqlens_q.shape[0] - 1
+    dO, Q, K, V, O = (_usable(t) for t in (dO, Q, K, V, O))
+    L = L.contiguous()
+    cu_q = cu_seqlens_q.to(device=Q.device, dtype=torch.int32).contiguous()
+    cu_k = cu_seqlens_k.to(device=Q.device, dtype=torch.int32).contiguous()
+    dQ = torch.empty((total_q, Hq, d), dtype=torch.float16, device=Q.device)
+    dK = torch.zeros((total_k, Hkv, d), dtype=torch.float16, device=Q.device)
+    dV = torch.zeros((total_k, Hkv, d), dtype=torch.float16, device=Q.device)
+    ws = _workspace(_lib.fal_bwd_varlen_workspace_size(num_seqs, total_q, total_k, Hq, d), Q.device)
+    st = lambda t: _strides(t, (None, 1, 0))
+    with torch.cuda.device(Q.device):
+        _check(_lib.fal_bwd_varlen(_ptr(dO), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L),
+                                   _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(cu_q), _ptr(cu_k),
+                                   num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
+                                   st(dO), st(Q), st(K), st(V), st(O), st(dQ), st(dK), st(dV),
+                                   float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(),
+                                   _stream(Q.device)))
+    return [dQ, dK, dV]
+
+
+def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_seqlens: torch.Tensor,
+           softmax_scale: float, mask_bias: Optional[torch.Tensor] = None, cache_layout: str = "bshd",
+           return_lse: bool = False):
+    """Split-K decode.  q [B,Hq,d] (one token per sequence); caches [B,S,Hkv,d]
+    (``cache_layout="bshd"``) or [B,Hkv,S,d] (``"bhsd"``); cache_seqlens int32 [B];
+    mask_bias optional fp32 [B,S] additive mask.  Returns O [B,Hq,d] (and L [B,Hq])."""
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_half_cuda(name, t)
+    if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise RuntimeError("decode expects q [B,Hq,d] and 4-D caches")
+    B, Hq, d = q.shape
+    if cache_layout == "bshd":
+        S, Hkv = k_cache.shape[1], k_cache.shape[2]
+        cdims = (0, 2, 1)
+    elif cache_layout == "bhsd":
+        Hkv, S = k_cache.shape[1], k_cache.shape[2]
+        cdims = (0, 1, 2)
+    else:
+        raise RuntimeError(f"unknown cache_layout {cache_layout!r}")
+    if k_cache.shape != v_cache.shape or k_cache.shape[0] != B or k_cache.shape[3] != d:
+        raise RuntimeError("k_cache / v_cache shape mismatch")
+    q, k_cache, v_cache = _usable(q), _usable(k_cache), _usable(v_cache)
+    seqlens = cache_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    bias = None
+    if mask_bias is not None:
+        bias = mask_bias.to(device=q.device, dtype=torch.float32)
+        if bias.stride(-1) != 1:
+            bias = bias.contiguous()
+    o = torch.empty((B, Hq, d), dtype=torch.float16, device=q.device)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
+    ws = _workspace(_lib.fal_decode_workspace_size(B, Hq, Hkv, S, d), q.device)
+    with torch.cuda.device(q.device):
+        _check(_lib.fal_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(seqlens), _ptr(bias),
+                               bias.stride(0) if bias is not None else 0, _ptr(o), _ptr(lse),
+                               B, Hq, Hkv, d, S,
+                               _strides(q, (0, 1, None)), _strides(k_cache, cdims), _strides(v_cache, cdims),
+                               _strides(o, (0, 1, None)), float(softmax_scale), _ptr(ws), ws.numel(),
+                               _stream(q.device)))
+    return (o, lse) if return_lse else o

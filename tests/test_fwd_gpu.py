@@ -1,0 +1,208 @@
+"""Forward parity on the GPU: the HIP kernel against the CPU oracle.
+
+Cases follow the reference's tests/test_flash_attn.py (TestForwardMHA :79-138,
+TestForwardGQA :145-193, TestLongSequences :486-547, TestNumericalStability
+:593-676) with seeded inputs and the stricter bound max|O - O_ref| <= 2e-3
+(fp64 oracle), plus the benchmark configurations C1 and C2.
+"""
+
+import math
+
+import pytest
+import torch
+
+from helpers import FWD_ATOL, max_abs, oracle_fwd, randn
+
+pytestmark = pytest.mark.gpu
+
+HEAD_DIMS = [32, 64, 96, 128, 256]
+
+
+def fa():
+    from flash_attn_legacy import flash_attention
+    return flash_attention
+
+
+def ext():
+    from flash_attn_legacy import hip_ext
+    return hip_ext
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [32, 64, 128, 256, 512])
+def test_seq_lengths(d, causal, N):
+    B, H = 2, 4
+    scale = 1.0 / math.sqrt(d)
+    q, k, v = (randn((B, H, N, d), seed=s, scale=0.3) for s in (1, 2, 3))
+    out = fa()(q, k, v, softmax_scale=scale, is_causal=causal)
+    ref, _ = oracle_fwd(q, k, v, scale, causal)
+    assert max_abs(out, ref) <= FWD_ATOL
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+@pytest.mark.parametrize("N", [1, 33, 65, 100, 200])
+@pytest.mark.parametrize("causal", [False, True])
+def test_non_power_of_2_and_lse(d, N, causal):
+    B, H = 1, 2
+    scale = 1.0 / math.sqrt(d)
+    q, k, v = (randn((B, H, N, d), seed=s) for s in (4, 5, 6))
+    o, lse = ext().forward(q, k, v, scale, causal)
+    ref_o, ref_lse = oracle_fwd(q, k, v, scale, causal)
+    assert max_abs(o, ref_o) <= FWD_ATOL
+    assert max_abs(lse, ref_lse) <= 1e-3
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_deterministic(d):
+    q, k, v = (randn((1, 4, 256, d), seed=s) for s in (7, 8, 9))
+    assert torch.equal(fa()(q, k, v), fa()(q, k, v))
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_single_token_is_v(d):
+    q, k, v = (randn((2, 4, 1, d), seed=s) for s in (10, 11, 12))
+    out = fa()(q, k, v)
+    torch.testing.assert_close(out, v, rtol=0, atol=1e-3)
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_uniform_attention(d):
+    q = torch.zeros(1, 1, 64, d, device="cuda", dtype=torch.float16)
+    k = torch.zeros_like(q)
+    v = randn((1, 1, 64, d), seed=13, scale=0.1)
+    out = fa()(q, k, v)
+    expected = v.float().mean(dim=2, keepdim=True).expand_as(v)
+    assert max_abs(out, expected) <= FWD_ATOL
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_batch_independence(d):
+    B, H, N = 4, 2, 128
+    scale = 1.0 / math.sqrt(d)
+    q, k, v = (randn((B, H, N, d), seed=s, scale=0.3) for s in (14, 15, 16))
+    full = fa()(q, k, v, softmax_scale=scale)
+    for b in range(B):
+        single = fa()(q[b:b + 1], k[b:b + 1], v[b:b + 1], softmax_scale=scale)
+        torch.testing.assert_close(full[b:b + 1], single, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 4), (8, 1), (4, 1), (4, 2)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa(d, hq, hkv, causal):
+    B, N = 2, 128
+    scale = 1.0 / math.sqrt(d)
+    q = randn((B, hq, N, d), seed=17, scale=0.3)
+    k = randn((B, hkv, N, d), seed=18, scale=0.3)
+    v = randn((B, hkv, N, d), seed=19, scale=0.3)
+    out = fa()(q, k, v, softmax_scale=scale, is_causal=causal)
+    ref, _ = oracle_fwd(q, k, v, scale, causal)
+    assert max_abs(out, ref) <= FWD_ATOL
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_mqa_equals_broadcast(d):
+    B, Hq, N = 2, 8, 128
+    q = randn((B, Hq, N, d), seed=20, scale=0.3)
+    k = randn((B, 1, N, d), seed=21, scale=0.3)
+    v = randn((B, 1, N, d), seed=22, scale=0.3)
+    out_mqa = fa()(q, k, v)
+    out_mha = fa()(q, k.expand(B, Hq, N, d), v.expand(B, Hq, N, d))
+    torch.testing.assert_close(out_mqa, out_mha, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_causal_first_row(d):
+    q, k = (randn((1, 2, 64, d), seed=s, scale=0.3) for s in (23, 24))
+    v = randn((1, 2, 64, d), seed=25)
+    out = fa()(q, k, v, is_causal=True)
+    torch.testing.assert_close(out[:, :, 0], v[:, :, 0], rtol=0, atol=1e-3)
+
+
+@pytest.mark.parametrize("d", HEAD_DIMS)
+def test_large_and_small_values(d):
+    scale = 1.0 / math.sqrt(d)
+    q, k = (randn((1, 2, 128, d), seed=s, scale=5.0) for s in (26, 27))
+    v = randn((1, 2, 128, d), seed=28, scale=0.1)
+    out = fa()(q, k, v, softmax_scale=scale)
+    assert torch.isfinite(out).all()
+    ref, _ = oracle_fwd(q, k, v, scale, False)
+    assert max_abs(out, ref) <= FWD_ATOL
+    q, k = (randn((1, 2, 128, d), seed=s, scale=1e-3) for s in (29, 30))
+    v = randn((1, 2, 128, d), seed=31, scale=0.5)
+    out = fa()(q, k, v)
+    assert max_abs(out, v.float().mean(dim=2, keepdim=True).expand_as(v)) <= FWD_ATOL
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_custom_and_negative_scale(d):
+    q, k, v = (randn((1, 2, 64, d), seed=s, scale=0.3) for s in (32, 33, 34))
+    for scale in (0.01, 1.0, -0.2):
+        out = fa()(q, k, v, softmax_scale=scale, is_causal=True)
+        ref, _ = oracle_fwd(q, k, v, scale, True)
+        assert max_abs(out, ref) <= FWD_ATOL
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_strided_inputs_no_copy(d):
+    """[B, N, H, d] storage viewed as [B, H, N, d] (the HF / module layout)."""
+    B, N, H = 2, 96, 4
+    base = randn((3, B, N, H, d), seed=35)
+    q, k, v = (base[i].transpose(1, 2) for i in range(3))
+    out = fa()(q, k, v, is_causal=True)
+    ref, _ = oracle_fwd(q, k, v, 1.0 / math.sqrt(d), True)
+    assert max_abs(out, ref) <= FWD_ATOL
+
+
+@pytest.mark.parametrize("nq,nk", [(64, 200), (200, 64), (1, 77)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_unequal_lengths_top_left(nq, nk, causal):
+    d = 64
+    q = randn((1, 4, nq, d), seed=36)
+    k, v = (randn((1, 2, nk, d), seed=s) for s in (37, 38))
+    o, lse = ext().forward(q, k, v, 0.125, causal)
+    ref_o, ref_lse = oracle_fwd(q, k, v, 0.125, causal)
+    assert max_abs(o, ref_o) <= FWD_ATOL
+    assert max_abs(lse, ref_lse) <= 1e-3
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("N", [1024, 2048, 4096])
+def test_long_sequences(d, N):
+    q, k, v = (randn((1, 2, N, d), seed=s) for s in (39, 40, 41))
+    out = fa()(q, k, v, is_causal=True)
+    assert torch.isfinite(out).all()
+    from oracle.torch_ref import ref_attention
+    ref = ref_attention(q.cpu(), k.cpu(), v.cpu(), 1.0 / math.sqrt(d), True)
+    assert max_abs(out, ref) <= FWD_ATOL
+
+
+def test_config_c1_full():
+    """C1: B=2, H=8, N=1024, d=64, causal, N(0,1) inputs, seed 0."""
+    B, H, N, d = 2, 8, 1024, 64
+    q, k, v = (randn((B, H, N, d), seed=s) for s in (0, 1, 2))
+    o, lse = ext().forward(q, k, v, 1.0 / math.sqrt(d), True)
+    ref_o, ref_lse = oracle_fwd(q, k, v, 1.0 / math.sqrt(d), True)
+    assert max_abs(o, ref_o) <= FWD_ATOL
+    assert max_abs(lse, ref_lse) <= 1e-3
+
+
+def test_config_c2_full_shape():
+    """C2 at full size (B=4, 32q/8kv heads, N=4096, d=128, causal); the heads of
+    KV groups 0 and 7 in batches 0 and 3 against the fp32 CPU formula, all outputs finite."""
+    B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
+    q = randn((B, Hq, N, d), seed=0)
+    k = randn((B, Hkv, N, d), seed=1)
+    v = randn((B, Hkv, N, d), seed=2)
+    scale = 1.0 / math.sqrt(d)
+    o, lse = ext().forward(q, k, v, scale, True)
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    from oracle.torch_ref import ref_attention
+    torch.set_num_threads(max(torch.get_num_threads(), 8))
+    for b in (0, 3):
+        for g in (0, Hkv - 1):
+            hs = slice(g * 4, g * 4 + 4)
+            ref = ref_attention(q[b:b + 1, hs].cpu(), k[b:b + 1, g:g + 1].cpu(), v[b:b + 1, g:g + 1].cpu(),
+                                scale, True)
+            assert max_abs(o[b:b + 1, hs], ref) <= FWD_ATOL, (b, g)
