@@ -1,0 +1,130 @@
+"""Varlen (packed sequences) parity on the GPU, forward and backward.
+
+Cases follow the reference's TestVarlen (tests/test_flash_attn.py:290-419): per-
+sequence oracle, GQA, single sequence equal to the batched path, many short
+sequences; plus the benchmark configuration C4 (16 lengths U[64, 4096], 32q/8kv
+heads, d=128, causal) and empty / unequal q-k segments.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import FWD_ATOL, GRAD_RTOL, cu_from_lens, max_abs, np64, randn, rel_err
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def varlen(q, k, v, cu_q, cu_k, mq, mk, scale, causal):
+    from flash_attn_legacy import flash_attn_varlen_func
+    return flash_attn_varlen_func(q, k, v, cu_q, cu_k, mq, mk, softmax_scale=scale, causal=causal)
+
+
+def fwd_check(lens_q, lens_k, hq, hkv, d, causal, seed=0):
+    tq, tk = sum(lens_q), sum(lens_k)
+    q = randn((tq, hq, d), seed=seed)
+    k = randn((tk, hkv, d), seed=seed + 1)
+    v = randn((tk, hkv, d), seed=seed + 2)
+    cu_q, cu_k = cu_from_lens(lens_q), cu_from_lens(lens_k)
+    scale = 1.0 / math.sqrt(d)
+    from flash_attn_legacy import hip_ext
+    o, lse = hip_ext.forward_varlen(q, k, v, cu_q, cu_k, max(lens_q), max(lens_k), scale, causal)
+    ref_o, ref_lse = orc.varlen_fwd(np64(q), np64(k), np64(v), cu_q.cpu().numpy(), cu_k.cpu().numpy(),
+                                    scale, causal)
+    assert o.shape == (tq, hq, d) and lse.shape == (tq, hq)
+    assert max_abs(o, torch.from_numpy(ref_o)) <= FWD_ATOL
+    fin = np.isfinite(ref_lse)
+    assert np.array_equal(np.isfinite(lse.cpu().numpy()), fin)
+    assert float(np.abs(lse.cpu().numpy()[fin] - ref_lse[fin]).max(initial=0)) <= 1e-3
+
+
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_correctness(d, causal):
+    fwd_check([32, 64, 48], [32, 64, 48], 4, 4, d, causal)
+
+
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
+def test_varlen_gqa(d):
+    fwd_check([64, 32], [64, 32], 8, 2, d, True)
+
+
+def test_varlen_single_sequence_matches_batched():
+    from flash_attn_legacy import flash_attention
+    H, N, d = 4, 128, 64
+    q, k, v = (randn((N, H, d), seed=s, scale=0.3) for s in (1, 2, 3))
+    cu = cu_from_lens([N])
+    out_varlen = varlen(q, k, v, cu, cu, N, N, 1.0 / math.sqrt(d), True)
+    qb, kb, vb = (t.permute(1, 0, 2).unsqueeze(0) for t in (q, k, v))
+    out_batch = flash_attention(qb, kb, vb, softmax_scale=1.0 / math.sqrt(d), is_causal=True)
+    torch.testing.assert_close(out_varlen, out_batch.squeeze(0).permute(1, 0, 2), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_many_short_and_empty_segments(causal):
+    fwd_check([16, 8, 32, 4, 24, 0, 1, 300, 129], [16, 8, 32, 4, 24, 0, 1, 300, 129], 2, 1, 64, causal)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_unequal_q_k_segments(causal):
+    fwd_check([10, 70, 130], [140, 33, 130], 4, 2, 128, causal)
+
+
+def bwd_check(lens_q, lens_k, hq, hkv, d, causal, seed=0):
+    tq, tk = sum(lens_q), sum(lens_k)
+    q = randn((tq, hq, d), seed=seed)
+    k = randn((tk, hkv, d), seed=seed + 1)
+    v = randn((tk, hkv, d), seed=seed + 2)
+    do = randn((tq, hq, d), seed=seed + 3)
+    cu_q, cu_k = cu_from_lens(lens_q), cu_from_lens(lens_k)
+    scale = 1.0 / math.sqrt(d)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    varlen(qg, kg, vg, cu_q, cu_k, max(lens_q), max(lens_k), scale, causal).backward(do)
+    ref = orc.varlen_bwd(np64(q), np64(k), np64(v), np64(do), cu_q.cpu().numpy(), cu_k.cpu().numpy(),
+                         scale, causal)
+    for name, g, r in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), ref):
+        e = rel_err(g, torch.from_numpy(r))
+        assert e <= GRAD_RTOL, f"{name} rel err {e:.3e}"
+
+
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_backward(d, causal):
+    bwd_check([32, 64, 48, 1], [32, 64, 48, 1], 4, 2, d, causal)
+
+
+def test_varlen_backward_unequal_segments():
+    bwd_check([10, 70, 0, 130], [140, 33, 5, 130], 4, 2, 64, True)
+
+
+def c4_lengths(seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return [int(x) for x in torch.randint(64, 4097, (16,), generator=g)]
+
+
+def test_config_c4_forward():
+    """C4 forward at full size; every sequence's heads of KV group 0 and 7 against the
+    fp32 CPU formula."""
+    from oracle.torch_ref import ref_attention
+    lens = c4_lengths()
+    tot, hq, hkv, d = sum(lens), 32, 8, 128
+    q = randn((tot, hq, d), seed=0)
+    k = randn((tot, hkv, d), seed=1)
+    v = randn((tot, hkv, d), seed=2)
+    cu = cu_from_lens(lens)
+    scale = 1.0 / math.sqrt(d)
+    o = varlen(q, k, v, cu, cu, max(lens), max(lens), scale, True)
+    assert torch.isfinite(o).all()
+    torch.set_num_threads(max(torch.get_num_threads(), 8))
+    c = cu.cpu().tolist()
+    for i in range(len(lens)):
+        for g in (0, hkv - 1):
+            hs = slice(g * 4, g * 4 + 4)
+            qi = q[c[i]:c[i + 1], hs].permute(1, 0, 2)[None].cpu()
+            ki = k[c[i]:c[i + 1], g:g + 1].permute(1, 0, 2)[None].cpu()
+            vi = v[c[i]:c[i + 1], g:g + 1].permute(1, 0, 2)[None].cpu()
+            ref = ref_attention(qi, ki, vi, scale, True)[0].permute(1, 0, 2)
+            assert max_abs(o[c[i]:c[i + 1], hs], ref) <= FWD_ATOL, (i, g)
