@@ -1,0 +1,219 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2]
+
+A step is one forward call of configuration C2 (GQA causal prefill: B=4, 32 query
+heads / 8 KV heads, N=4096, d=128, fp16 N(0,1) inputs from seed 0) -- the
+configuration the headline metric is quoted on.  The line printed at the end is
+one JSON object:
+
+* ``value``: C2 forward TFLOP/s (FA2 flop convention: 4*B*Hq*N^2*d, halved for
+  causal), inputs resident in HBM, K steps between two device synchronisations;
+* ``roofline``: the forward kernel's algorithmic flops per launch over its
+  average launch time (HIP events on the launch stream, same timed region),
+  against the 2.5 PFLOP/s dense fp16 MFMA peak; ``traffic`` comes from the
+  committed rocprofv3 counter summary when present;
+* ``cpu_baseline``: fp32 PyTorch attention (the reference's own test formula) on
+  this host's CPU cores over a bounded sample of the same workload;
+* ``extra``: the other configurations measured the same way -- C1 forward, C3
+  backward (2.5x forward flops), C4 varlen forward, C5 split-K decode (KV bytes
+  read, GB/s against 8 TB/s HBM).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-attention-legacy_amd"))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "attn fwd/bwd TFLOP/s (% fp16 MFMA peak); decode KV GB/s (% HBM peak)"
+
+
+def randn(shape, seed, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).half().to(device)
+
+
+def fwd_flops(b, hq, nq, nk, d, causal):
+    f = 4.0 * b * hq * nq * nk * d
+    return f / 2 if causal else f
+
+
+def time_steps(fn, steps, warmup):
+    """Run `fn` warmup times, then time `steps` calls.  Returns (wall ms/step,
+    event ms/step) -- the events are recorded on the current stream, which is the
+    stream the kernels are launched on."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, e0.elapsed_time(e1) / steps
+
+
+def bench_c2(steps, warmup):
+    from flash_attn_legacy import hip_ext
+    B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
+    q, k, v = randn((B, Hq, N, d), 0), randn((B, Hkv, N, d), 1), randn((B, Hkv, N, d), 2)
+    scale = 1.0 / math.sqrt(d)
+    wall, ev = time_steps(lambda: hip_ext.forward(q, k, v, scale, True), steps, warmup)
+    return wall, ev, fwd_flops(B, Hq, N, N, d, True)
+
+
+def bench_extra(steps, warmup):
+    from flash_attn_legacy import hip_ext
+    out = {}
+    # C1
+    q, k, v = (randn((2, 8, 1024, 64), s) for s in (0, 1, 2))
+    _, ev = time_steps(lambda: hip_ext.forward(q, k, v, 0.125, True), steps, warmup)
+    f = fwd_flops(2, 8, 1024, 1024, 64, True)
+    out["c1_fwd"] = {"tflops": round(f / ev / 1e9, 2), "ms": round(ev, 4),
+                     "frac_peak": round(f / ev / 1e9 / PEAK_FP16_TFLOPS, 4)}
+    # C3 backward
+    B, H, N, d = 2, 16, 2048, 128
+    q, k, v, do = (randn((B, H, N, d), s) for s in (0, 1, 2, 3))
+    scale = 1.0 / math.sqrt(d)
+    o, lse = hip_ext.forward(q, k, v, scale, True)
+    _, ev = time_steps(lambda: hip_ext.backward(do, q, k, v, o, lse, scale, True), steps, warmup)
+    f = 2.5 * fwd_flops(B, H, N, N, d, True)
+    out["c3_bwd"] = {"tflops": round(f / ev / 1e9, 2), "ms": round(ev, 4),
+                     "frac_peak": round(f / ev / 1e9 / PEAK_FP16_TFLOPS, 4)}
+    del q, k, v, do, o, lse
+    # C4 varlen forward
+    g = torch.Generator().manual_seed(0)
+    lens = [int(x) for x in torch.randint(64, 4097, (16,), generator=g)]
+    tot = sum(lens)
+    q, k, v = randn((tot, 32, 128), 0), randn((tot, 8, 128), 1), randn((tot, 8, 128), 2)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
+    mx = max(lens)
+    _, ev = time_steps(lambda: hip_ext.forward_varlen(q, k, v, cu, cu, mx, mx, scale, True), steps, warmup)
+    f = sum(fwd_flops(1, 32, n, n, 128, True) for n in lens)
+    out["c4_varlen_fwd"] = {"tflops": round(f / ev / 1e9, 2), "ms": round(ev, 4),
+                            "frac_peak": round(f / ev / 1e9 / PEAK_FP16_TFLOPS, 4), "total_tokens": tot}
+    del q, k, v
+    # C5 decode
+    g = torch.Generator().manual_seed(0)
+    lens = [int(x) for x in torch.randint(1024, 32769, (32,), generator=g)]
+    S = max(lens)
+    q = randn((32, 32, 128), 1)
+    kc, vc = randn((32, S, 8, 128), 2), randn((32, S, 8, 128), 3)
+    seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    _, ev = time_steps(lambda: hip_ext.decode(q, kc, vc, seq, scale), steps, warmup)
+    nbytes = sum(lens) * 8 * 128 * 2 * 2
+    out["c5_decode"] = {"gbs": round(nbytes / ev / 1e6, 1), "ms": round(ev, 4),
+                        "frac_peak": round(nbytes / ev / 1e6 / PEAK_HBM_GBS, 4), "kv_bytes": nbytes}
+    return out
+
+
+def cpu_baseline(budget_s=15.0):
+    """fp32 PyTorch attention (reference tests/test_flash_attn.py:19-32) on the host CPU,
+    over (batch, KV-group) slices of C2 -- 4 query heads x N=4096 x d=128, causal --
+    until `budget_s` seconds have been spent.  Rate in TFLOP/s (same flop convention)."""
+    from oracle.torch_ref import ref_attention
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 4, N, d), generator=gen).half()
+    k = torch.randn((1, 1, N, d), generator=gen).half()
+    v = torch.randn((1, 1, N, d), generator=gen).half()
+    scale = 1.0 / math.sqrt(d)
+    ref_attention(q[:, :, :256], k[:, :, :256], v[:, :, :256], scale, True)   # warm the thread pool
+    done, t0 = 0, time.perf_counter()
+    while True:
+        ref_attention(q, k, v, scale, True)
+        done += 1
+        if time.perf_counter() - t0 >= budget_s or done >= B * Hkv:
+            break
+    dt = time.perf_counter() - t0
+    flops = done * fwd_flops(1, 4, N, N, d, True)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{done} of the 32 (batch, KV-group) slices of C2 (4 query heads x N=4096 x d=128, "
+                      f"causal), fp32 torch on CPU, {dt:.1f} s; os.cpu_count()={threads}; cpu={cpu_model}"}
+
+
+def load_traffic():
+    """HBM bytes per C2 forward launch from the committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", "fwd_c2_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["c2", "all"], default="all")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(every box has one MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    wall, ev, flops = bench_c2(a.steps, a.warmup)
+    value = flops / (wall * 1e-3) / 1e12
+    achieved = flops / (ev * 1e-3) / 1e12
+    extra = bench_extra(max(5, a.steps // 2), max(2, a.warmup // 2)) if a.only == "all" else {}
+    traffic = load_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "C2 fwd GQA causal prefill", "batch": 4, "heads_q": 32, "heads_kv": 8,
+                   "seq_len": 4096, "head_dim": 128, "causal": True, "inputs": "fp16 N(0,1) seed 0"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                     "traffic": traffic, "kernel": "fwd_kernel<128,4,64,true>",
+                     "flops_per_launch": flops},
+        "cpu_baseline": None if a.no_cpu else cpu_baseline(),
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -58,6 +58,14 @@ int launch_status(hipError_t e, const char* what) {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// softmax_scale * log2(e) with its magnitude kept away from 0, so masked scores
+// (+-inf) never meet a zero factor.
+float signed_scale_log2(float scale) {
+  const float a = scale * kLog2e;
+  if (std::fabs(a) >= 1e-30f) return a;
+  return scale < 0.f ? -1e-30f : 1e-30f;
+}
+
 float scale_log2(float scale) {
   // |scale| * log2(e); clamped away from 0 so masked scores (-inf) stay -inf.
   const float a = std::fabs(scale) * kLog2e;
@@ -114,8 +122,7 @@ int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, in
   p.l_sb = heads_q * seqlen_q; p.l_sh = seqlen_q; p.l_ss = 1;
   p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
   p.Nq = (int)seqlen_q; p.Nk = (int)seqlen_k;
-  p.scale_log2 = scale_log2(softmax_scale);
-  p.negate_q = softmax_scale < 0.f;
+  p.scale_log2 = signed_scale_log2(softmax_scale);
   const int bm = fwd_block_m((int)head_dim);
   p.n_qtiles = cdiv((int)seqlen_q, bm);
   const int64_t nblocks = (int64_t)p.n_qtiles * batch * heads_q;
@@ -179,8 +186,7 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
   p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
   p.l_sb = 0; p.l_sh = 1; p.l_ss = heads_q;
   p.B = 1; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
-  p.scale_log2 = scale_log2(softmax_scale);
-  p.negate_q = softmax_scale < 0.f;
+  p.scale_log2 = signed_scale_log2(softmax_scale);
   p.cu_q = cu_seqlens_q;
   p.cu_k = cu_seqlens_k;
   p.work = work;

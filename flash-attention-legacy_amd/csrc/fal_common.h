@@ -105,4 +105,54 @@ __device__ __forceinline__ half8 cvt8(const f32x16& c, int t) {
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Sum of 8 fp16 values into an fp32 accumulator (v_dot2 with ones).
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float sum8_f16(half8 v, float acc) {
+  const half2v one = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2(half2v{v[2 * j], v[2 * j + 1]}, one, acc, false);
+  return acc;
+}
+
+// 16-byte global -> LDS copy that bypasses VGPRs (gfx950 global_load_lds_dwordx4).
+// Lane i of the wave writes bytes [16 i, 16 i + 16) of `lds_wave_base`, which must be
+// the same for all lanes.  Completion is tracked by vmcnt (see wait_vmcnt0).
+__device__ __forceinline__ void global_to_lds16(const half_t* src, half_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
+}
+// Raw buffer resource over `nbytes` bytes at `base` (loads past the end return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+// 16-byte buffer -> LDS copy (buffer_load_dwordx4 ... lds); lane i writes bytes
+// [16 i, 16 i + 16) of `lds_wave_base` (uniform across the wave).
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rs, int voffset, half_t* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds_wave_base), 16,
+                                           voffset, 0, 0, 0);
+}
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Row-major LDS tile of D fp16 columns stored as 16-byte chunks with an XOR swizzle
+// of the chunk index by the row.  The swizzle makes both access patterns used on
+// these tiles free of bank conflicts:
+//   * 16 consecutive rows, one chunk each (MFMA A/B fragments, ds_read_b128);
+//   * 4 consecutive rows (first row a multiple of 4) x 4 aligned chunks
+//     (ds_read_b64_tr_b16 of a 32-column block by a 32-lane half-wave).
+// swz(r) only depends on r mod 16, so row offsets that are multiples of 16 keep it.
+template <int D>
+struct SwizzledTile {
+  static constexpr int CPR = D / 8;   // chunks per row
+  __device__ static int swz(int r) {
+    if constexpr (D == 32) return (r >> 2) & 3;
+    else if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else if constexpr (D == 96) return 0;
+    else return ((r & 3) << 2) | ((r >> 2) & 3);
+  }
+  // element offset of logical chunk c of row r
+  __device__ static int offset(int r, int c) { return (r * CPR + (c ^ swz(r))) * 8; }
+  // logical chunk held by physical chunk cp of row r (the swizzle is an involution)
+  __device__ static int logical_chunk(int r, int cp) { return cp ^ swz(r); }
+};
+
 }  // namespace fal

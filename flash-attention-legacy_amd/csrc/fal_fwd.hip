@@ -17,23 +17,38 @@
 //   V^T comes from the row-major V tile through ds_read_b64_tr_b16;
 // * causal tiles above the diagonal are never visited; fully-masked waves inside a
 //   diagonal tile skip their MFMAs.
+#include <type_traits>
+
 #include "fal_kernels.h"
 
 namespace fal {
 
+// Tunables (compile-time): minimum waves per SIMD the register budget must allow,
+// KV tile width for head_dim <= 128, lazy-rescale threshold (log2 units).
+#ifndef FAL_FWD_WPE
+#define FAL_FWD_WPE 2
+#endif
+#ifndef FAL_FWD_BN
+#define FAL_FWD_BN 64
+#endif
+#ifndef FAL_FWD_RESCALE_THRESHOLD
+#define FAL_FWD_RESCALE_THRESHOLD 8.0f
+#endif
+
 template <int D, int NW, int BN, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64)
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? FAL_FWD_WPE : 1, 8)))
 fwd_kernel(FwdParams p) {
+  using TL = SwizzledTile<D>;
   constexpr int BM = NW * 32;
   constexpr int KS = D / 16;        // MFMA k-steps over the head dim
   constexpr int NKB = BN / 32;      // 32-key blocks per tile
   constexpr int DB = D / 32;        // 32-wide blocks of the output head dim
-  constexpr int LDK = D + 8;        // padded LDS row (elements)
-  constexpr int CHUNKS = BN * D / 8;                 // 16-byte chunks per K (or V) tile
-  constexpr int CPT = (CHUNKS + NW * 64 - 1) / (NW * 64);
-  constexpr int CPR = D / 8;                         // chunks per row
+  constexpr int CPR = TL::CPR;      // 16-byte chunks per row
+  constexpr int PART = BN * CPR * 8;          // elements of one K (or V) tile
+  constexpr int IPT = BN * CPR / (NW * 64);   // direct-to-LDS loads per wave per part
+  static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(16))) half_t smem[2 * 2 * BN * LDK];
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * 2 * PART];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -87,130 +102,177 @@ fwd_kernel(FwdParams p) {
   const int row = m0 + w * 32 + l32;
   half8 qreg[KS];
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
+  for (int t = 0; t < KS; ++t)
     qreg[t] = row < nq ? load_h8(qbase + (int64_t)row * p.q_ss + t * 16 + hh * 8) : zero_h8();
-    if (p.negate_q) qreg[t] = -qreg[t];
-  }
-  const float c = p.scale_log2;   // |scale| * log2(e); the sign was folded into Q
+  const float c = p.scale_log2;   // softmax_scale * log2(e), signed
 
   // ---- key range ----
   const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
   const int ntiles = cdiv(kend, BN);
+  // tiles below this index need no masking for any row of the workgroup
+  const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
+
+  // ---- per-lane addressing of the swizzled tiles ----
+  const int ws = __builtin_amdgcn_readfirstlane(w);   // wave index as a scalar
+  int kvo[IPT], vvo[IPT], lrow[IPT], lcol[IPT];        // direct-load sources (byte offsets in the tile)
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int pch = (ws * IPT + i) * 64 + lane;
+    lrow[i] = pch / CPR;
+    lcol[i] = TL::logical_chunk(lrow[i], pch % CPR) * 8;
+    kvo[i] = (int)(lrow[i] * p.k_ss + lcol[i]) * 2;
+    vvo[i] = (int)(lrow[i] * p.v_ss + lcol[i]) * 2;
+  }
+  int kaddr[KS];                     // K fragment (row l32, chunk 2t+hh) for 32-key block 0
+#pragma unroll
+  for (int t = 0; t < KS; ++t) kaddr[t] = TL::offset(l32, 2 * t + hh);
+  int vaddr[2][DB];                  // transposed V reads: rows hf*8 + hh*4 + i/4 of each 16-key step
+  {
+    const int i = lane & 15;
+    const int rl = hh * 4 + (i >> 2);
+    const int cl = 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) vaddr[hf][db] = TL::offset(hf * 8 + rl, db * 4 + cl) + 4 * (lane & 1);
+  }
+
+  // Tile `tile` of K and V into LDS buffer `buf` without passing through VGPRs.  The
+  // buffer resource starts at the tile's first row (scalar); per-lane offsets are
+  // fixed.  Rows past the end of the sequence are clamped to the last row (their
+  // scores are masked and their probabilities are zero).
+  auto load_tile = [&](int tile, int buf) {
+    const int n0 = tile * BN;
+    const bool tail = n0 + BN > nk;
+    half_t* kdst = smem + buf * 2 * PART + ws * IPT * 64 * 8;
+    half_t* vdst = kdst + PART;
+    const uint32_t kbytes = (uint32_t)min((int64_t)(nk - n0) * p.k_ss * 2, (int64_t)0x7fffffff);
+    const uint32_t vbytes = (uint32_t)min((int64_t)(nk - n0) * p.v_ss * 2, (int64_t)0x7fffffff);
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase + (int64_t)n0 * p.k_ss, kbytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase + (int64_t)n0 * p.v_ss, vbytes);
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      int ko = kvo[i], vo = vvo[i];
+      if (tail) {
+        const int r = min(lrow[i], nk - 1 - n0);
+        ko = (int)(r * p.k_ss + lcol[i]) * 2;
+        vo = (int)(r * p.v_ss + lcol[i]) * 2;
+      }
+      buffer_to_lds16(krs, ko, kdst + i * 64 * 8);
+      buffer_to_lds16(vrs, vo, vdst + i * 64 * 8);
+    }
+  };
 
   f32x16 oacc[DB];
 #pragma unroll
   for (int i = 0; i < DB; ++i) oacc[i] = zero_f16();
-  float m_run = -INFINITY;   // running max, log2 domain
-  float l_run = 0.f;         // running sum (this lane's keys only)
+  float m_run = -INFINITY;   // running max, log2 domain (may lag the true max by < threshold)
+  float l_run = 0.f;         // running sum of this lane's keys
+  const bool pos = c >= 0.f;
+  const float mval = pos ? -INFINITY : INFINITY;   // masked raw score
 
-  u32x4 kpre[CPT], vpre[CPT];
-  auto fetch = [&](int tile) {
-    const int n0 = tile * BN;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int ch = tid + i * NW * 64;
-      const int r = ch / CPR;
-      const int cc = (ch % CPR) * 8;
-      const bool ok = (CHUNKS % (NW * 64) == 0 || ch < CHUNKS) && (n0 + r < nk);
-      kpre[i] = ok ? load_u4(kbase + (int64_t)(n0 + r) * p.k_ss + cc) : u32x4{0, 0, 0, 0};
-      vpre[i] = ok ? load_u4(vbase + (int64_t)(n0 + r) * p.v_ss + cc) : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto stash = [&](int buf) {
-    half_t* ks = smem + buf * 2 * BN * LDK;
-    half_t* vs = ks + BN * LDK;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int ch = tid + i * NW * 64;
-      if (CHUNKS % (NW * 64) == 0 || ch < CHUNKS) {
-        const int r = ch / CPR;
-        const int cc = (ch % CPR) * 8;
-        store_u4(ks + r * LDK + cc, kpre[i]);
-        store_u4(vs + r * LDK + cc, vpre[i]);
-      }
-    }
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    stash(0);
-  }
-  __syncthreads();
-
-  const int wrow_lo = m0 + w * 32;        // first query row of this wave
-  const int vofs = tr_offset(lane, LDK);
-
-  for (int j = 0; j < ntiles; ++j) {
-    if (j + 1 < ntiles) fetch(j + 1);
+  auto tile_body = [&](auto masked, int j, int buf) {
+    constexpr bool MASK = decltype(masked)::value;
     const int n0 = j * BN;
-    const half_t* ks = smem + (j & 1) * 2 * BN * LDK;
-    const half_t* vs = ks + BN * LDK;
-
-    if (!CAUSAL || n0 <= wrow_lo + 31) {
-      // S^T = K Q^T : one 32x32 block per 32 keys
-      f32x16 sacc[NKB];
+    const half_t* ks = smem + buf * 2 * PART;
+    const half_t* vs = ks + PART;
+    // S^T = K Q^T, the 32-key blocks interleaved so consecutive MFMAs are independent
+    f32x16 sacc[NKB];
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        sacc[kb] = zero_f16();
+    for (int kb = 0; kb < NKB; ++kb) sacc[kb] = zero_f16();
 #pragma unroll
-        for (int t = 0; t < KS; ++t) {
-          const half8 a = load_h8(ks + (kb * 32 + l32) * LDK + t * 16 + hh * 8);
-          sacc[kb] = mfma32(a, qreg[t], sacc[kb]);
+    for (int t = 0; t < KS; ++t)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        sacc[kb] = mfma32(load_h8(ks + kaddr[t] + kb * 32 * CPR * 8), qreg[t], sacc[kb]);
+    if (MASK) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = n0 + kb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+          if (key >= nk || (CAUSAL && key > row)) sacc[kb][i] = mval;
         }
-      }
-      // masking (only on tiles that touch the sequence end or the diagonal)
-      const bool need_mask = (n0 + BN > nk) || (CAUSAL && n0 + BN - 1 > wrow_lo);
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = n0 + kb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
-            if (key >= nk || (CAUSAL && key > row)) sacc[kb][i] = -INFINITY;
-          }
-      }
-      // online softmax for this lane's query row
-      float mx = -INFINITY;
+    }
+    // row max of scale*s (scale may be negative: reduce with min then)
+    float mx;
+    if (pos) {
+      mx = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb][i]);
       mx = pair_max(mx);
-      const float m_new = fmaxf(m_run, mx * c);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-      float rs = 0.f;
+    } else {
+      mx = INFINITY;
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(fmaf(sacc[kb][i], c, -m_use));
-          sacc[kb][i] = e;
-          rs += e;
-        }
-      l_run = fmaf(l_run, alpha, rs);
+        for (int i = 0; i < 16; ++i) mx = fminf(mx, sacc[kb][i]);
+      mx = -pair_max(-mx);
+    }
+    const float m_new = fmaxf(m_run, mx * c);
+    // Lazy rescale: move the reference max only when it grew by more than the
+    // threshold somewhere in the wave, so p stays <= 2^threshold and the O/l
+    // rescale runs on few tiles.
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run + FAL_FWD_RESCALE_THRESHOLD)) {
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-      // O^T += V^T P^T
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const half8 pb = cvt8(sacc[kb], t2);
-          const int krow = kb * 32 + t2 * 16;
-#pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const half8 va = lds_kslab_tr(vs + vofs + db * 32, krow, hh, LDK);
-            oacc[db] = mfma32(va, pb, oacc[db]);
-          }
-        }
     }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    // P^T = exp2(s*c - m), straight into the B operand of O^T += V^T P^T
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[kb][i] = fast_exp2(fmaf(sacc[kb][i], c, -m_use));
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const half8 pb = cvt8(sacc[kb], t2);
+        l_run = sum8_f16(pb, l_run);
+        const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const half4 lo = lds_read_tr(vs + vaddr[0][db] + kofs);
+          const half4 hi = lds_read_tr(vs + vaddr[1][db] + kofs);
+          oacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
+        }
+      }
+  };
+  // One pipeline step: wait for tile j, prefetch tile j+1 into the other buffer, consume j.
+  auto step = [&](auto masked, int j, int buf) {
+    wait_vmcnt0();
+    __syncthreads();                       // tile j visible; tile j-1 reads finished
+    if (j + 1 < ntiles) load_tile(j + 1, buf ^ 1);
+    tile_body(masked, j, buf);
+  };
 
-    if (j + 1 < ntiles) stash((j + 1) & 1);
+  if (ntiles > 0) load_tile(0, 0);
+  // Tiles that need no mask for any row of the workgroup: straight-line, unrolled by
+  // two so both LDS buffer offsets are constants.
+  int j = 0;
+  for (; j + 1 < nfull; j += 2) {
+    step(std::false_type{}, j, 0);
+    step(std::false_type{}, j + 1, 1);
+  }
+  if (j < nfull) {
+    step(std::false_type{}, j, 0);
+    ++j;
+  }
+  // Diagonal and tail tiles; waves whose rows all precede the tile only keep the
+  // pipeline (barrier + prefetch) going.
+  const int wrow_hi = m0 + w * 32 + 31;   // last query row of this wave
+  for (; j < ntiles; ++j) {
+    wait_vmcnt0();
     __syncthreads();
+    if (j + 1 < ntiles) load_tile(j + 1, (j + 1) & 1);
+    if (!CAUSAL || j * BN <= wrow_hi) tile_body(std::true_type{}, j, j & 1);
   }
 
   // ---- epilogue: normalise, write O and L ----
@@ -229,7 +291,7 @@ fwd_kernel(FwdParams p) {
       }
     if (hh == 0) {
       float L = -INFINITY;
-      if (m_run != -INFINITY) L = (m_run + fast_log2(fmaxf(l_tot, 1e-20f))) * kLn2;
+      if (l_tot > 0.f) L = (m_run + fast_log2(l_tot)) * kLn2;
       lbase[(int64_t)row * p.l_ss] = L;
     }
   }
@@ -283,7 +345,7 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int tile, int n
 template <int D>
 struct FwdCfg {
   static constexpr int NW = 4;
-  static constexpr int BN = (D >= 256) ? 32 : 64;
+  static constexpr int BN = (D >= 256) ? 32 : FAL_FWD_BN;
 };
 
 template <int D>

@@ -25,8 +25,7 @@ struct FwdParams {
   int64_t l_sb, l_sh, l_ss;
   int B, Hq, Hkv, Nq, Nk;
   int n_qtiles;
-  float scale_log2;   // |softmax_scale| * log2(e)
-  int negate_q;       // softmax_scale < 0
+  float scale_log2;   // softmax_scale * log2(e), signed, |.| >= 1e-30
   const int* cu_q;
   const int* cu_k;
   const int2* work;

@@ -30,7 +30,9 @@ from typing import List, Optional
 import torch
 
 _LIB_NAME = "libfal_hip.so"
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+# FLASH_ATTN_LEGACY_LIB selects another build of the same library (e.g. a tuning variant).
+_LIB_PATH = os.environ.get("FLASH_ATTN_LEGACY_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
 
 _VP = ctypes.c_void_p
 _I64 = ctypes.c_int64
