@@ -74,8 +74,22 @@ def build(jobs: int | None = None, verbose: bool = False, out: str = OUT, define
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
+    _check_stubs(tmp)
     os.replace(tmp, out)
     return out
+
+
+def _check_stubs(lib: str) -> None:
+    """Fail if a kernel's host launch stub is referenced but not defined: hipcc's host
+    pass can drop a kernel instantiation without a diagnostic, which would only show
+    up as a dlopen error on the GPU host."""
+    nm = shutil.which("nm")
+    if not nm:
+        return
+    r = subprocess.run([nm, "-D", "--undefined-only", lib], capture_output=True, text=True)
+    missing = [l.split()[-1] for l in r.stdout.splitlines() if "__device_stub__" in l]
+    if missing:
+        raise RuntimeError(f"{lib}: undefined kernel stubs (host pass dropped them): {missing}")
 
 
 def main() -> int:

@@ -351,7 +351,8 @@ size_t fal_decode_workspace_size(int64_t batch, int64_t heads_q, int64_t heads_k
                                  (int)(max_seqlen_k > 0 ? max_seqlen_k : 1));
   const int64_t ms = (max_seqlen_k + chunk - 1) / chunk < 1 ? 1 : (max_seqlen_k + chunk - 1) / chunk;
   const size_t parts = (size_t)batch * heads_q * ms;
-  return align256(parts * head_dim * sizeof(float)) + align256(parts * sizeof(float));
+  return align256(parts * head_dim * sizeof(float)) + align256(parts * sizeof(float)) +
+         align256((size_t)batch * ms * sizeof(int2));
 }
 
 int fal_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
@@ -395,9 +396,12 @@ int fal_decode(const void* q, const void* k_cache, const void* v_cache, const in
   const size_t parts = (size_t)batch * heads_q * p.max_splits;
   p.part_o = static_cast<float*>(workspace);
   p.part_m = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(parts * head_dim * sizeof(float)));
+  p.work = reinterpret_cast<const int2*>(static_cast<char*>(workspace) + align256(parts * head_dim * sizeof(float)) +
+                                         align256(parts * sizeof(float)));
   p.scale_log2 = scale_log2(softmax_scale);
   p.negate_q = softmax_scale < 0.f;
-  if (batch > 65535) return fail(FAL_ERR_INVALID, "batch too large for one launch");
+  if ((int64_t)batch * p.max_splits * heads_kv * ((heads_q / heads_kv + 15) / 16) > 0x7fffffff)
+    return fail(FAL_ERR_INVALID, "batch too large for one launch");
   return launch_status(launch_decode(p, (int)head_dim, static_cast<hipStream_t>(stream)), "fal_decode");
 }
 

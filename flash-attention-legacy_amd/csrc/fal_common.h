@@ -127,9 +127,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 // 16-byte buffer -> LDS copy (buffer_load_dwordx4 ... lds); lane i writes bytes
 // [16 i, 16 i + 16) of `lds_wave_base` (uniform across the wave).
+// AUX: cache-policy bits of the load.
+template <int AUX = 0>
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rs, int voffset, half_t* lds_wave_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds_wave_base), 16,
-                                           voffset, 0, 0, 0);
+                                           voffset, 0, 0, AUX);
 }
 __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

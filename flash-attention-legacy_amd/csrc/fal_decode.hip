@@ -16,162 +16,239 @@
 // * The waves' (max, sum, O) are merged in LDS and the workgroup writes one
 //   normalised partial O (fp32) and its log2-domain LSE.
 // Combine kernel: one wave per (sequence, query head) merges its splits.
+#include <type_traits>
+
 #include "fal_kernels.h"
 
 namespace fal {
 
-constexpr int kDecNW = 4;
+// Waves per workgroup.  Each wave streams its own 32-row steps of the split with a
+// two-step prefetch: K rows straight into MFMA operand registers, V rows into a
+// wave-private LDS ring (read back transposed).  No workgroup barrier until the
+// final merge.
+#ifndef FAL_DEC_NW
+#define FAL_DEC_NW 4
+#endif
+#ifndef FAL_DEC_VAUX
+#define FAL_DEC_VAUX 0   // cache-policy bits of the V (LDS-direct) loads
+#endif
+
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// Combine with the value of the lanes 16 and 32 apart (the four 16-lane rows).
+__device__ __forceinline__ float rows4_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  return pair_max(x);
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  return pair_sum(x);
+}
+
+// V slice: 16 cache rows x D columns in 16-byte chunks, chunk index XOR-swizzled by
+// the row so a transposed read of 16 rows x 32 bytes spreads over all banks.
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+  return D == 96 ? (r & 3) : (r & ((D / 8 < 16 ? D / 8 : 16) - 1));
+}
 
 template <int D, int NW>
 __global__ void __launch_bounds__(NW * 64)
 decode_split_kernel(DecodeParams p) {
-  constexpr int KS = D / 16;
-  constexpr int DB = D / 32;
-  constexpr int LDV = D + 8;
-  __shared__ __attribute__((aligned(16))) half_t v_s[NW][32 * LDV];
-  __shared__ float m_s[NW][32];
-  __shared__ float l_s[NW][32];
-  __shared__ float o_s[32 * D];
+  constexpr int KS = D / 32;              // 16x16x32 k-steps over the head dim
+  constexpr int DBN = D / 16;             // 16-wide output blocks
+  constexpr int CPR = D / 8;              // 16-byte chunks per row
+  constexpr int SLICE = 16 * CPR * 8;     // elements of one 16-row V slice
+  constexpr int VI = 16 * CPR / 64;       // direct loads per V slice
+  constexpr int LPS = 2 * KS + 2 * VI;    // loads issued per 32-row step
+  static_assert(16 * CPR % 64 == 0, "slice must be whole load instructions");
+  __shared__ __attribute__((aligned(1024))) half_t vsm[NW][4 * SLICE];   // 2 steps x 2 slices
+  __shared__ float m_s[NW][16];
+  __shared__ float l_s[NW][16];
+  __shared__ float inv_s[16];
+  __shared__ float o_s[16 * D];
 
-  const int split = blockIdx.x;
-  const int hkv = blockIdx.y;
-  const int b = blockIdx.z;
+  const int nhg = cdiv(p.Hq / p.Hkv, 16);
+  const int heads_tiles = p.Hkv * nhg;
+  const int2 wk = p.work[blockIdx.x / heads_tiles];
+  if (wk.x < 0) return;
+  const int b = wk.x;
+  const int split = wk.y;
+  const int hkv = (blockIdx.x % heads_tiles) / nhg;
+  const int hg = (blockIdx.x % heads_tiles) % nhg;
   const int L = p.seqlens[b];
   const int k_begin = split * p.chunk;
   if (k_begin >= L) return;
   const int k_end = min(L, k_begin + p.chunk);
+  const int nsteps = cdiv(k_end - k_begin, 32);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int l32 = lane & 31;
-  const int hh = lane >> 5;
+  const int ws = __builtin_amdgcn_readfirstlane(w);
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;
   const int G = p.Hq / p.Hkv;
+  const int hbase = hkv * G + hg * 16;           // first query head of this tile
+  const int nh = min(16, G - hg * 16);
 
-  for (int i = tid; i < 32 * D; i += NW * 64) o_s[i] = 0.f;
+  for (int i = tid; i < 16 * D; i += NW * 64) o_s[i] = 0.f;
 
-  // queries of the group as the B operand (n = head, k = head dim)
+  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
+  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
+  // K: lane loads row l16, columns t*32 + g4*8 .. +8 of each slice (A operand layout)
+  const int kvo = (int)(l16 * p.k_ss + g4 * 8) * 2;
+  // V: load instruction I of a slice fills chunks [I*64, I*64+64)
+  int vvo[VI];
+#pragma unroll
+  for (int I = 0; I < VI; ++I) {
+    const int pch = I * 64 + lane;
+    const int r = pch / CPR;
+    const int cch = (pch % CPR) ^ vswz<D>(r);
+    vvo[I] = (int)(r * p.v_ss + cch * 8) * 2;
+  }
+  half_t* vring = &vsm[ws][0];
+
+  // one 32-row step = two 16-row slices
+  half8 kreg[2][2][KS];
+  auto issue = [&](int step, int buf) {
+    const int r0 = k_begin + step * 32;
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const int rs = r0 + sl * 16;
+      const int64_t left = (int64_t)max(k_end - rs, 0);
+      const __amdgpu_buffer_rsrc_t krs =
+          make_rsrc(kbase + (int64_t)rs * p.k_ss, (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff));
+      const __amdgpu_buffer_rsrc_t vrs =
+          make_rsrc(vbase + (int64_t)rs * p.v_ss, (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff));
+#pragma unroll
+      for (int t = 0; t < KS; ++t)
+        kreg[buf][sl][t] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo + t * 64, 0, 0));
+#pragma unroll
+      for (int I = 0; I < VI; ++I)
+        buffer_to_lds16<FAL_DEC_VAUX>(vrs, vvo[I], vring + (buf * 2 + sl) * SLICE + I * 64 * 8);
+    }
+  };
+  // this wave's steps: ws, ws + NW, ...
+  int j = ws;
+  if (j < nsteps) issue(j, 0);
+  if (j + NW < nsteps) issue(j + NW, 1);
+
+  // queries of the head tile as the B operand (n = head, k = head dim)
   half8 qreg[KS];
-  const half_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)(hkv * G + l32) * p.q_sh;
+  const half_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)(hbase + l16) * p.q_sh;
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    qreg[t] = l32 < G ? load_h8(qrow + t * 16 + hh * 8) : zero_h8();
+    qreg[t] = l16 < nh ? load_h8(qrow + t * 32 + g4 * 8) : zero_h8();
     if (p.negate_q) qreg[t] = -qreg[t];
   }
   const float c = p.scale_log2;
-  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
-  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
   const float* bias = p.bias ? p.bias + (int64_t)b * p.bias_sb : nullptr;
 
-  f32x16 oacc[DB];
+  // transposed V reads: lane i of 16-lane group g4 reads row 4*g4 + i/4, columns
+  // db*16 + 4*(i%4) .. +4 of a slice
+  const int vr = 4 * g4 + (l16 >> 2);
+  const int vrbase = vr * CPR * 8 + 4 * (l16 & 1);
+  const int vrc0 = ((l16 >> 1) & 1) ^ vswz<D>(vr);   // chunk of block 0; block db is vrc0 ^ 2*db
+#define VRD(db) (vrbase + ((vrc0 ^ (2 * (db))) << 3))
+
+  f32x4 oacc[DBN];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) oacc[i] = zero_f16();
+  for (int i = 0; i < DBN; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  half8 kc[KS];
-  u32x4 vc[KS];
-  auto load_slice = [&](int s0, half8* kk, u32x4* vv) {
-    const int r = s0 + l32;
-    const bool ok = r < k_end;
+  auto step = [&](auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    if (j + NW < nsteps) wait_vmcnt<LPS>();
+    else wait_vmcnt<0>();
+    // S^T for the two slices (element i: row 16*sl + 4*g4 + i, head l16)
+    f32x4 s[2];
 #pragma unroll
-    for (int t = 0; t < KS; ++t) {
-      kk[t] = ok ? load_h8(kbase + (int64_t)r * p.k_ss + t * 16 + hh * 8) : zero_h8();
-      vv[t] = ok ? load_u4(vbase + (int64_t)r * p.v_ss + t * 16 + hh * 8) : u32x4{0, 0, 0, 0};
+    for (int sl = 0; sl < 2; ++sl) {
+      s[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KS; ++t) s[sl] = mfma16(kreg[buf][sl][t], qreg[t], s[sl]);
     }
-  };
-
-  half_t* vs = v_s[w];
-  const int vofs = tr_offset(lane, LDV);
-  int s0 = k_begin + w * 32;
-  if (s0 < k_end) load_slice(s0, kc, vc);
-  for (; s0 < k_end; s0 += NW * 32) {
-    half8 kn[KS];
-    u32x4 vn[KS];
-    const int s1 = s0 + NW * 32;
-    if (s1 < k_end) load_slice(s1, kn, vn);
-
-#pragma unroll
-    for (int t = 0; t < KS; ++t) store_u4(vs + l32 * LDV + t * 16 + hh * 8, vc[t]);
-
-    f32x16 s = zero_f16();
-#pragma unroll
-    for (int t = 0; t < KS; ++t) s = mfma32(kc[t], qreg[t], s);
-    // element i: cache row s0 + (i/4)*8 + hh*4 + i%4, head l32
+    const int r0 = k_begin + j * 32;
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = s0 + (i >> 2) * 8 + hh * 4 + (i & 3);
-      float t = s[i] * c;
-      if (bias && r < k_end) t = fmaf(bias[r], kLog2e, t);
-      if (r >= k_end) t = -INFINITY;
-      s[i] = t;
-      mx = fmaxf(mx, t);
-    }
-    mx = pair_max(mx);
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = r0 + sl * 16 + 4 * g4 + i;
+        float x = s[sl][i] * c;
+        if (bias && r < k_end) x = fmaf(bias[r], kLog2e, x);
+        if (r >= k_end) x = -INFINITY;
+        s[sl][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = rows4_max(mx);
     const float m_new = fmaxf(m_run, mx);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
     m_run = m_new;
-    float rs = 0.f;
+    half8 pb;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float e = fast_exp2(s[i] - m_use);
-      s[i] = e;
-      rs += e;
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pb[sl * 4 + i] = (half_t)fast_exp2(s[sl][i] - m_use);
+    l_run = sum8_f16(pb, l_run * alpha);
+#pragma unroll
+    for (int db = 0; db < DBN; ++db) oacc[db] *= alpha;
+    // O^T += V^T P^T over the 32 rows
+    const half_t* v0 = vring + (buf * 2) * SLICE;
+#pragma unroll
+    for (int db = 0; db < DBN; ++db) {
+      const half4 lo = lds_read_tr(v0 + VRD(db));
+      const half4 hi = lds_read_tr(v0 + SLICE + VRD(db));
+      oacc[db] = mfma16(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
     }
-    l_run = fmaf(l_run, alpha, rs);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      const half8 pb = cvt8(s, t2);
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        oacc[db] = mfma32(lds_kslab_tr(vs + vofs + db * 32, t2 * 16, hh, LDV), pb, oacc[db]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int t = 0; t < KS; ++t) {
-      kc[t] = kn[t];
-      vc[t] = vn[t];
-    }
+    // LDS reads of this buffer must finish before the next loads overwrite it
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (j + 2 * NW < nsteps) issue(j + 2 * NW, buf);
+    j += NW;
+  };
+  // two steps per trip so the register ring index is a compile-time constant
+  while (j < nsteps) {
+    step(std::integral_constant<int, 0>{});
+    if (j >= nsteps) break;
+    step(std::integral_constant<int, 1>{});
   }
 
-  // ---- merge the waves ----
-  __shared__ float inv_s[32];
-  const float l_tot = pair_sum(l_run);
-  if (hh == 0) {
-    m_s[w][l32] = m_run;
-    l_s[w][l32] = l_tot;
+  // ---- merge: heads are lanes l16; rows split over the four 16-lane groups ----
+  const float l_tot = rows4_sum(l_run);
+  if (lane < 16) {
+    m_s[w][l16] = m_run;
+    l_s[w][l16] = l_tot;
   }
   __syncthreads();
   float M = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < NW; ++i) M = fmaxf(M, m_s[i][l32]);
+  for (int i = 0; i < NW; ++i) M = fmaxf(M, m_s[i][l16]);
   const float M_use = (M == -INFINITY) ? 0.f : M;
-  const float wscale = fast_exp2(m_run - M_use);   // this wave's weight for head l32
-  if (l32 < G) {
+  const float wscale = fast_exp2(m_run - M_use);
+  if (l16 < nh) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < DBN; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = db * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
-        atomicAdd(&o_s[l32 * D + d], oacc[db][i] * wscale);
-      }
+      for (int i = 0; i < 4; ++i) atomicAdd(&o_s[l16 * D + db * 16 + 4 * g4 + i], oacc[db][i] * wscale);
   }
-  const int64_t pbase = ((int64_t)b * p.Hq + hkv * G) * p.max_splits + split;
-  if (w == 0 && hh == 0 && l32 < G) {
+  const int64_t pbase = ((int64_t)b * p.Hq + hbase) * p.max_splits + split;
+  if (w == 0 && lane < nh) {
     float Lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) Lsum += l_s[i][l32] * fast_exp2(m_s[i][l32] - M_use);
-    inv_s[l32] = Lsum > 0.f ? 1.f / Lsum : 0.f;
-    p.part_m[pbase + (int64_t)l32 * p.max_splits] = (Lsum > 0.f) ? M_use + fast_log2(Lsum) : -INFINITY;
+    for (int i = 0; i < NW; ++i) Lsum += l_s[i][l16] * fast_exp2(m_s[i][l16] - M_use);
+    inv_s[l16] = Lsum > 0.f ? 1.f / Lsum : 0.f;
+    p.part_m[pbase + (int64_t)l16 * p.max_splits] = (Lsum > 0.f) ? M_use + fast_log2(Lsum) : -INFINITY;
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += NW * 64) {
+  for (int i = tid; i < nh * D; i += NW * 64) {
     const int h = i / D, d = i % D;
     p.part_o[(pbase + (int64_t)h * p.max_splits) * D + d] = o_s[h * D + d] * inv_s[h];
   }
@@ -217,17 +294,73 @@ decode_combine_kernel(DecodeParams p) {
     p.lse[(int64_t)b * p.Hq + hq] = (wsum > 0.f && M != -INFINITY) ? (M + fast_log2(wsum)) * kLn2 : -INFINITY;
 }
 
+#ifndef FAL_DEC_CHUNK
+#define FAL_DEC_CHUNK 2048
+#endif
+
+// Cache rows per split: start from FAL_DEC_CHUNK and halve (down to one tile) until
+// the grid has at least ~4 workgroups per CU for the longest sequence.
+// Work list of (sequence, split) items, longest first: every full chunk, then the
+// partial last chunks by descending length (64 length buckets).  Heavy workgroups
+// start first, so the kernel does not end on a tail of long splits.  Built on the
+// device from cache_seqlens; unused trailing slots get (-1, -1).
+__global__ void __launch_bounds__(1024)
+decode_schedule_kernel(const int* __restrict__ seqlens, int B, int chunk, int2* __restrict__ work, int capacity) {
+  __shared__ int hist[64], cur[64], full_total, full_cur;
+  for (int i = threadIdx.x; i < 64; i += blockDim.x) hist[i] = 0;
+  if (threadIdx.x == 0) full_total = 0;
+  __syncthreads();
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const int L = max(seqlens[b], 0);
+    if (L / chunk) atomicAdd(&full_total, L / chunk);
+    if (L % chunk) atomicAdd(&hist[(L % chunk) * 64 / chunk], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = full_total;
+    for (int k = 63; k >= 0; --k) {
+      cur[k] = acc;
+      acc += hist[k];
+    }
+    full_cur = 0;
+    hist[0] = acc;   // total items
+  }
+  __syncthreads();
+  const int total = hist[0];
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const int L = max(seqlens[b], 0);
+    const int nf = L / chunk;
+    if (nf) {
+      const int pos = atomicAdd(&full_cur, nf);
+      for (int s = 0; s < nf; ++s)
+        if (pos + s < capacity) work[pos + s] = make_int2(b, s);
+    }
+    if (L % chunk) {
+      const int pos = atomicAdd(&cur[(L % chunk) * 64 / chunk], 1);
+      if (pos < capacity) work[pos] = make_int2(b, nf);
+    }
+  }
+  for (int i = total + threadIdx.x; i < capacity; i += blockDim.x) work[i] = make_int2(-1, -1);
+}
+
 int decode_chunk(int d, int B, int Hkv, int max_seqlen) {
   (void)d;
-  int spw = 4;
-  while (spw > 1 && (long)B * Hkv * cdiv(max_seqlen, kDecNW * 32 * spw) < 2048) spw >>= 1;
-  return kDecNW * 32 * spw;
+  const int tile = FAL_DEC_NW * 32;
+  int chunk = FAL_DEC_CHUNK;
+  while (chunk > tile && (long)B * Hkv * cdiv(max_seqlen, chunk) < 1024) chunk >>= 1;
+  return chunk < tile ? tile : chunk;
 }
 
 template <int D>
 static hipError_t launch_decode_d(const DecodeParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((decode_split_kernel<D, kDecNW>), dim3(p.max_splits, p.Hkv, p.B), dim3(kDecNW * 64), 0,
-                     st, p);
+  const int nhg = cdiv(p.Hq / p.Hkv, 16);
+  const int capacity = p.B * p.max_splits;
+  hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(1024), 0, st, p.seqlens, p.B, p.chunk,
+                     const_cast<int2*>(p.work), capacity);
+  hipError_t e0 = hipGetLastError();
+  if (e0 != hipSuccess) return e0;
+  hipLaunchKernelGGL((decode_split_kernel<D, FAL_DEC_NW>), dim3((unsigned)capacity * p.Hkv * nhg),
+                     dim3(FAL_DEC_NW * 64), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.Hq, p.B), dim3(64), 0, st, p);

@@ -31,6 +31,19 @@ namespace fal {
 #ifndef FAL_FWD_BN
 #define FAL_FWD_BN 64
 #endif
+#ifndef FAL_FWD_ABLATE
+#define FAL_FWD_ABLATE 0
+#endif
+#ifndef FAL_FWD_KDEPTH
+#define FAL_FWD_KDEPTH 2
+#endif
+#if FAL_FWD_SETPRIO
+#define FAL_PRIO_MFMA() __builtin_amdgcn_s_setprio(1)
+#define FAL_PRIO_VALU() __builtin_amdgcn_s_setprio(0)
+#else
+#define FAL_PRIO_MFMA() ((void)0)
+#define FAL_PRIO_VALU() ((void)0)
+#endif
 #ifndef FAL_FWD_RESCALE_THRESHOLD
 #define FAL_FWD_RESCALE_THRESHOLD 8.0f
 #endif
@@ -113,15 +126,22 @@ fwd_kernel(FwdParams p) {
   const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
 
   // ---- per-lane addressing of the swizzled tiles ----
+  // Load instruction i of wave ws fills LDS chunks [(i*NW + ws)*64, +64): rows
+  // row0(I) .. of the tile, I = i*NW + ws.  Each instruction gets its own buffer
+  // resource starting at its first row, so rows past the end of the sequence fall
+  // outside the resource and are written as zeros; per-lane offsets are then
+  // independent of the tile (and, for head_dim 32/64/128, of i as well).
   const int ws = __builtin_amdgcn_readfirstlane(w);   // wave index as a scalar
-  int kvo[IPT], vvo[IPT], lrow[IPT], lcol[IPT];        // direct-load sources (byte offsets in the tile)
+  int kvo[IPT], vvo[IPT];
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
-    const int pch = (ws * IPT + i) * 64 + lane;
-    lrow[i] = pch / CPR;
-    lcol[i] = TL::logical_chunk(lrow[i], pch % CPR) * 8;
-    kvo[i] = (int)(lrow[i] * p.k_ss + lcol[i]) * 2;
-    vvo[i] = (int)(lrow[i] * p.v_ss + lcol[i]) * 2;
+    const int I = i * NW + ws;
+    const int row0 = I * 64 / CPR;
+    const int pch = I * 64 + lane;
+    const int r = pch / CPR;
+    const int c = TL::logical_chunk(r, pch % CPR);
+    kvo[i] = (int)((r - row0) * p.k_ss + c * 8) * 2;
+    vvo[i] = (int)((r - row0) * p.v_ss + c * 8) * 2;
   }
   int kaddr[KS];                     // K fragment (row l32, chunk 2t+hh) for 32-key block 0
 #pragma unroll
@@ -137,29 +157,20 @@ fwd_kernel(FwdParams p) {
       for (int db = 0; db < DB; ++db) vaddr[hf][db] = TL::offset(hf * 8 + rl, db * 4 + cl) + 4 * (lane & 1);
   }
 
-  // Tile `tile` of K and V into LDS buffer `buf` without passing through VGPRs.  The
-  // buffer resource starts at the tile's first row (scalar); per-lane offsets are
-  // fixed.  Rows past the end of the sequence are clamped to the last row (their
-  // scores are masked and their probabilities are zero).
+  // Tile `tile` of K and V into LDS buffer `buf` without passing through VGPRs.
   auto load_tile = [&](int tile, int buf) {
     const int n0 = tile * BN;
-    const bool tail = n0 + BN > nk;
-    half_t* kdst = smem + buf * 2 * PART + ws * IPT * 64 * 8;
+    half_t* kdst = smem + buf * 2 * PART;
     half_t* vdst = kdst + PART;
-    const uint32_t kbytes = (uint32_t)min((int64_t)(nk - n0) * p.k_ss * 2, (int64_t)0x7fffffff);
-    const uint32_t vbytes = (uint32_t)min((int64_t)(nk - n0) * p.v_ss * 2, (int64_t)0x7fffffff);
-    const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase + (int64_t)n0 * p.k_ss, kbytes);
-    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase + (int64_t)n0 * p.v_ss, vbytes);
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
-      int ko = kvo[i], vo = vvo[i];
-      if (tail) {
-        const int r = min(lrow[i], nk - 1 - n0);
-        ko = (int)(r * p.k_ss + lcol[i]) * 2;
-        vo = (int)(r * p.v_ss + lcol[i]) * 2;
-      }
-      buffer_to_lds16(krs, ko, kdst + i * 64 * 8);
-      buffer_to_lds16(vrs, vo, vdst + i * 64 * 8);
+      const int I = i * NW + ws;
+      const int r0 = n0 + I * 64 / CPR;           // first sequence row of this instruction
+      const int64_t left = (int64_t)max(nk - r0, 0);
+      const uint32_t kb = (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff);
+      const uint32_t vb = (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff);
+      buffer_to_lds16(make_rsrc(kbase + (int64_t)r0 * p.k_ss, kb), kvo[i], kdst + I * 64 * 8);
+      buffer_to_lds16(make_rsrc(vbase + (int64_t)r0 * p.v_ss, vb), vvo[i], vdst + I * 64 * 8);
     }
   };
 
@@ -176,15 +187,31 @@ fwd_kernel(FwdParams p) {
     const int n0 = j * BN;
     const half_t* ks = smem + buf * 2 * PART;
     const half_t* vs = ks + PART;
-    // S^T = K Q^T, the 32-key blocks interleaved so consecutive MFMAs are independent
+    // S^T = K Q^T, the 32-key blocks interleaved so consecutive MFMAs are independent.
+    // K fragments are read FAL_FWD_KDEPTH k-steps ahead of the MFMAs that use them.
     f32x16 sacc[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) sacc[kb] = zero_f16();
+    half8 kfrag[KS][NKB];
 #pragma unroll
-    for (int t = 0; t < KS; ++t)
+    for (int t = 0; t < FAL_FWD_KDEPTH && t < KS; ++t)
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-        sacc[kb] = mfma32(load_h8(ks + kaddr[t] + kb * 32 * CPR * 8), qreg[t], sacc[kb]);
+      for (int kb = 0; kb < NKB; ++kb) kfrag[t][kb] = load_h8(ks + kaddr[t] + kb * 32 * CPR * 8);
+    __builtin_amdgcn_sched_group_barrier(0x100, (FAL_FWD_KDEPTH < KS ? FAL_FWD_KDEPTH : KS) * NKB, 0);
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      if (t + FAL_FWD_KDEPTH < KS) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+          kfrag[t + FAL_FWD_KDEPTH][kb] = load_h8(ks + kaddr[t + FAL_FWD_KDEPTH] + kb * 32 * CPR * 8);
+        __builtin_amdgcn_sched_group_barrier(0x100, NKB, 0);   // the reads ...
+      }
+      FAL_PRIO_MFMA();
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) sacc[kb] = mfma32(kfrag[t][kb], qreg[t], sacc[kb]);
+      __builtin_amdgcn_sched_group_barrier(0x008, NKB, 0);     // ... then the MFMAs of step t
+    }
+    FAL_PRIO_VALU();
     if (MASK) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
@@ -194,6 +221,19 @@ fwd_kernel(FwdParams p) {
           if (key >= nk || (CAUSAL && key > row)) sacc[kb][i] = mval;
         }
     }
+#if FAL_FWD_ABLATE == 1
+    for (int kb = 0; kb < NKB; ++kb)
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const half8 pb = cvt8(sacc[kb], t2);
+        const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
+        for (int db = 0; db < DB; ++db) {
+          const half4 lo = lds_read_tr(vs + vaddr[0][db] + kofs);
+          const half4 hi = lds_read_tr(vs + vaddr[1][db] + kofs);
+          oacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
+        }
+      }
+    return;
+#endif
     // row max of scale*s (scale may be negative: reduce with min then)
     float mx;
     if (pos) {
@@ -237,19 +277,30 @@ fwd_kernel(FwdParams p) {
         const half8 pb = cvt8(sacc[kb], t2);
         l_run = sum8_f16(pb, l_run);
         const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
+#if FAL_FWD_ABLATE == 2
+        oacc[0][0] += (float)pb[0] + (float)pb[7];
+        (void)kofs;
+#else
+        FAL_PRIO_MFMA();
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const half4 lo = lds_read_tr(vs + vaddr[0][db] + kofs);
           const half4 hi = lds_read_tr(vs + vaddr[1][db] + kofs);
           oacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
         }
+#endif
       }
+    FAL_PRIO_VALU();
   };
   // One pipeline step: wait for tile j, prefetch tile j+1 into the other buffer, consume j.
   auto step = [&](auto masked, int j, int buf) {
+#if FAL_FWD_ABLATE != 4
     wait_vmcnt0();
     __syncthreads();                       // tile j visible; tile j-1 reads finished
+#endif
+#if FAL_FWD_ABLATE != 3
     if (j + 1 < ntiles) load_tile(j + 1, buf ^ 1);
+#endif
     tile_body(masked, j, buf);
   };
 

@@ -77,6 +77,7 @@ struct DecodeParams {
   float* lse;               // optional [B, Hq] natural-log LSE
   float* part_o;            // [B, Hq, max_splits, d] fp32 partial outputs
   float* part_m;            // [B, Hq, max_splits] partial log2-domain LSE
+  const int2* work;         // [B * max_splits] (sequence, split) items, longest first
   int64_t q_sb, q_sh;
   int64_t k_sb, k_ss, k_sh;
   int64_t v_sb, v_ss, v_sh;
