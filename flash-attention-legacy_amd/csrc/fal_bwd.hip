@@ -347,6 +347,318 @@ bwd_kernel(BwdParams p) {
   }
 }
 
+// Scheduling fence between MFMA steps of the head_dim-128 kernel: keeps the compiler
+// from hoisting every operand read of a phase at once (which overflows the 256-register
+// budget of two waves per SIMD).
+#ifndef FAL_BWD_FENCES
+#define FAL_BWD_FENCES 1
+#endif
+#if FAL_BWD_FENCES
+#define FAL_BWD_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define FAL_BWD_FENCE() ((void)0)
+#endif
+
+// --------------------------------------------------------------------------
+// KV-outer kernel for head_dim 64 and 128: 8 waves = 4 key groups x 2 query halves.
+//
+// A workgroup owns BN = 128 keys (wave w: keys 32*(w%4) .., query half w/4) and walks
+// query tiles of 64 rows; per tile each wave computes S/P/dP/dS for its 32 keys x 32
+// rows, accumulates dV^T += dO^T P and dK^T += Q^T dS in registers, stages dS^T in
+// LDS, and after a barrier computes one 32x32 block of dQ = dS K for the tile, added
+// to the fp32 accumulator with atomics.  K and V are read from swizzled LDS tiles
+// (B operands of S, dP and dQ).  Q/dO tiles are double-buffered in LDS through
+// direct buffer loads.  For causal attention a workgroup takes key tiles kt and
+// n-1-kt, so all workgroups do the same amount of work.  The two query halves'
+// dK/dV partials are summed in LDS.
+// --------------------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(512)
+bwd2_kernel(BwdParams p) {
+  using TL = SwizzledTile<D>;
+  using TS = SwizzledTile<64>;            // dS^T tile: 64 query columns per key row
+  constexpr int NW = 8, BN = 128, BMQ = 64;
+  constexpr int KS = D / 16;
+  constexpr int DWB = D / 32;
+  constexpr int CPR = TL::CPR;
+  constexpr int KPART = BN * CPR * 8;     // elements of the K (or V) tile
+  constexpr int QPART = BMQ * CPR * 8;    // elements of one Q (or dO) tile
+  constexpr int KIPT = BN * CPR / (NW * 64);
+  constexpr int QIPT = BMQ * CPR / (NW * 64);
+  static_assert(BMQ * CPR % (NW * 64) == 0, "Q tile must split evenly over the waves");
+  static_assert(2 * 2 * QPART * 2 >= 4 * 32 * D * 4, "dK/dV reduction reuses the Q/dO buffers");
+
+  __shared__ __attribute__((aligned(1024))) half_t ks_s[KPART];
+  __shared__ __attribute__((aligned(1024))) half_t vs_s[KPART];
+  __shared__ __attribute__((aligned(1024))) half_t qd_s[2 * 2 * QPART];   // [buffer][Q, dO]
+  __shared__ __attribute__((aligned(1024))) half_t dst_s[BN * BMQ];
+  __shared__ float l_s[2][BMQ];
+  __shared__ float d_s[2][BMQ];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int ws = __builtin_amdgcn_readfirstlane(w);
+  const int kg = w & 3;                   // key group
+  const int qh = w >> 2;                  // query half
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  // ---- work item: up to two key tiles of one (batch, KV head) ----
+  int b, hkv, q_off, k_off, nq, nk, kt_a, kt_b;
+  if (p.cu_q) {
+    const int2 wk = p.work[blockIdx.x];
+    if (wk.x < 0) return;
+    hkv = blockIdx.y;
+    b = 0;
+    kt_a = wk.y;
+    kt_b = -1;
+    q_off = p.cu_q[wk.x];
+    nq = p.cu_q[wk.x + 1] - q_off;
+    k_off = p.cu_k[wk.x];
+    nk = p.cu_k[wk.x + 1] - k_off;
+  } else {
+    const int total = gridDim.x;
+    int id = blockIdx.x;
+    if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+    const int nitems = CAUSAL ? (p.n_ktiles + 1) / 2 : p.n_ktiles;
+    const int it = id % nitems;
+    const int bh = id / nitems;
+    b = bh / p.Hkv;
+    hkv = bh % p.Hkv;
+    kt_a = it;
+    kt_b = (CAUSAL && p.n_ktiles - 1 - it != it) ? p.n_ktiles - 1 - it : -1;
+    q_off = 0;
+    k_off = 0;
+    nq = p.Nq;
+    nk = p.Nk;
+  }
+  const int G = p.Hq / p.Hkv;
+  const float c = p.scale_log2;
+  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
+  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
+
+  // per-lane direct-load offsets (instruction i of wave ws fills chunks [(i*NW+ws)*64, +64))
+  // (in-tile offsets are 32-bit: buffer offsets are, and a tile spans < 2^31 bytes)
+  auto dl_offset = [&](int i, int64_t ss) {
+    const int I = i * NW + ws;
+    const int pch = I * 64 + lane;
+    const int r = pch / CPR;
+    return ((r - I * 64 / CPR) * (int)ss + TL::logical_chunk(r, pch % CPR) * 8) * 2;
+  };
+  // Fragment reads (row l32 of a 32-row block, chunk 2t+hh) and transposed reads
+  // (rows hf*8 + hh*4 + i/4 of a 16-row step, 32-column block db) of the swizzled
+  // tiles.  The swizzle is an XOR on the chunk index, so every address is a lane
+  // base XOR a compile-time chunk offset; keeping only the bases saves registers.
+  const int fbase = TL::offset(l32, hh);
+  int trb[2], sdb[2];
+  {
+    const int i = lane & 15;
+    const int rl = hh * 4 + (i >> 2);
+    const int cl = 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      trb[hf] = TL::offset(hf * 8 + rl, cl);
+      sdb[hf] = TS::offset(hf * 8 + rl, qh * 4 + cl) + 4 * (lane & 1);
+    }
+  }
+  const int tr_lo = 4 * (lane & 1);
+  auto faddr = [&](int t) { return fbase ^ ((2 * t) << 3); };
+  // 8 k-slots for rows row0.. (multiple of 16) of a swizzled D-column tile, block db
+  auto trk = [&](const half_t* base, int db, int row0) {
+    const half4 lo = lds_read_tr(base + (trb[0] ^ ((db * 4) << 3)) + tr_lo + row0 * CPR * 8);
+    const half4 hi = lds_read_tr(base + (trb[1] ^ ((db * 4) << 3)) + tr_lo + row0 * CPR * 8);
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  auto trs = [&](int row0) {   // the same for the dS^T tile (64 columns, block qh)
+    const half4 lo = lds_read_tr(dst_s + sdb[0] + row0 * 64);
+    const half4 hi = lds_read_tr(dst_s + sdb[1] + row0 * 64);
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+
+  const int nqt = cdiv(nq, BMQ);
+  const int dq_db = w & 3;                // dQ block of this wave: rows qh*32.., cols dq_db*32..
+
+  for (int tile_i = 0; tile_i < 2; ++tile_i) {
+    const int kt = tile_i == 0 ? kt_a : kt_b;
+    if (kt < 0) break;
+    const int n0 = kt * BN;
+    if (n0 >= nk) continue;
+    const int kw0 = n0 + kg * 32;
+    const int key = kw0 + l32;
+
+    __syncthreads();   // previous tile's readers of the LDS tiles are done
+#pragma unroll
+    for (int i = 0; i < KIPT; ++i) {
+      const int I = i * NW + ws;
+      const int r0 = n0 + I * 64 / CPR;
+      const uint32_t kb = (uint32_t)min((int64_t)max(nk - r0, 0) * p.k_ss * 2, (int64_t)0x7fffffff);
+      buffer_to_lds16(make_rsrc(kbase + (int64_t)r0 * p.k_ss, kb), dl_offset(i, p.k_ss), ks_s + I * 64 * 8);
+      const uint32_t vb = (uint32_t)min((int64_t)max(nk - r0, 0) * p.v_ss * 2, (int64_t)0x7fffffff);
+      buffer_to_lds16(make_rsrc(vbase + (int64_t)r0 * p.v_ss, vb), dl_offset(i, p.v_ss), vs_s + I * 64 * 8);
+    }
+
+    f32x16 dk_acc[DWB], dv_acc[DWB];
+#pragma unroll
+    for (int i = 0; i < DWB; ++i) {
+      dk_acc[i] = zero_f16();
+      dv_acc[i] = zero_f16();
+    }
+    const int qt0 = CAUSAL ? (n0 / BMQ) : 0;
+
+    for (int g = 0; g < G; ++g) {
+      const int hq = hkv * G + g;
+      const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
+      const half_t* dobase = p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
+      const float* lbase = p.lse + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
+      const float* dbase_p = p.delta + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
+      float* qabase = p.dq_acc + (int64_t)b * p.dqa_sb + (int64_t)hq * p.dqa_sh + (int64_t)q_off * p.dqa_ss;
+
+      float lpre = 0.f, dpre = 0.f;
+      auto fetch = [&](int qt, int buf) {
+        const int q0 = qt * BMQ;
+#pragma unroll
+        for (int i = 0; i < QIPT; ++i) {
+          const int I = i * NW + ws;
+          const int r0 = q0 + I * 64 / CPR;
+          const int64_t left = (int64_t)max(nq - r0, 0);
+          buffer_to_lds16(make_rsrc(qbase + (int64_t)r0 * p.q_ss, (uint32_t)min(left * p.q_ss * 2, (int64_t)0x7fffffff)),
+                          dl_offset(i, p.q_ss), qd_s + (buf * 2 + 0) * QPART + I * 64 * 8);
+          buffer_to_lds16(make_rsrc(dobase + (int64_t)r0 * p.do_ss, (uint32_t)min(left * p.do_ss * 2, (int64_t)0x7fffffff)),
+                          dl_offset(i, p.do_ss), qd_s + (buf * 2 + 1) * QPART + I * 64 * 8);
+        }
+        if (tid < BMQ) {
+          float lv = INFINITY, dv = 0.f;
+          if (q0 + tid < nq) {
+            const int o = tid * (int)p.l_ss;
+            const float L = (lbase + (int64_t)q0 * p.l_ss)[o];
+            lv = (L == -INFINITY) ? INFINITY : L * kLog2e;
+            dv = (dbase_p + (int64_t)q0 * p.l_ss)[o];
+          }
+          lpre = lv;
+          dpre = dv;
+        }
+      };
+
+      if (qt0 < nqt) fetch(qt0, 0);
+      for (int qt = qt0; qt < nqt; ++qt) {
+        const int buf = (qt - qt0) & 1;
+        const int q0 = qt * BMQ;
+        wait_vmcnt0();
+        if (tid < BMQ) {
+          l_s[buf][tid] = lpre;
+          d_s[buf][tid] = dpre;
+        }
+        __syncthreads();                  // barrier A: tile qt in LDS; dQ readers of qt-1 done
+        if (qt + 1 < nqt) fetch(qt + 1, buf ^ 1);
+        const half_t* q_s = qd_s + (buf * 2 + 0) * QPART + qh * 32 * CPR * 8;
+        const half_t* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
+        const int qr0 = q0 + qh * 32;     // first query row of this wave's half
+        if (!CAUSAL || qr0 + 31 >= kw0) {
+          // S = Q K^T and dP = dO V^T
+          f32x16 s = zero_f16(), dp = zero_f16();
+#pragma unroll
+          for (int t = 0; t < KS; ++t) {
+            const int fa = faddr(t);
+            s = mfma32(load_h8(q_s + fa), load_h8(ks_s + fa + kg * 32 * CPR * 8), s);
+            dp = mfma32(load_h8(do_s + fa), load_h8(vs_s + fa + kg * 32 * CPR * 8), dp);
+            FAL_BWD_FENCE();
+          }
+          // P and dS; element i: query qr0 + (i/4)*8 + hh*4 + i%4, key `key`
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const f32x4 lv = *reinterpret_cast<const f32x4*>(&l_s[buf][qh * 32 + g4 * 8 + hh * 4]);
+            const f32x4 dv = *reinterpret_cast<const f32x4*>(&d_s[buf][qh * 32 + g4 * 8 + hh * 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int i = g4 * 4 + e;
+              const int qrow = qr0 + g4 * 8 + hh * 4 + e;
+              float pv = fast_exp2(fmaf(s[i], c, -lv[e]));
+              if (key >= nk || qrow >= nq || (CAUSAL && key > qrow)) pv = 0.f;
+              s[i] = pv;
+              dp[i] = pv * (dp[i] - dv[e]);
+            }
+          }
+          // dV^T += dO^T P ; dK^T += Q^T dS
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const half8 pb = cvt8(s, ks);
+            const half8 sb = cvt8(dp, ks);
+#pragma unroll
+            for (int db = 0; db < DWB; ++db) {
+              dv_acc[db] = mfma32(trk(do_s, db, ks * 16), pb, dv_acc[db]);
+              dk_acc[db] = mfma32(trk(q_s, db, ks * 16), sb, dk_acc[db]);
+              FAL_BWD_FENCE();
+            }
+          }
+          // dS^T (fp16) into LDS: row = key (tile-local), 64 query columns
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)dp[g4 * 4 + e];
+            const int col = qh * 32 + g4 * 8 + hh * 4;
+            *reinterpret_cast<half4*>(dst_s + TS::offset(kg * 32 + l32, col >> 3) + (col & 7)) = h;
+          }
+        }
+        __syncthreads();                  // barrier B: dS^T complete
+        // dQ[q0 + qh*32 .. +32, dq_db*32 .. +32] += dS K over the active key steps
+        if (dq_db < DWB) {
+          const int qrb = q0 + qh * 32;
+          f32x16 acc = zero_f16();
+          for (int ks = 0; ks < BN / 16; ++ks) {
+            if (CAUSAL && qrb + 31 < n0 + (ks >> 1) * 32) break;
+            acc = mfma32(trs(ks * 16), trk(ks_s, dq_db, ks * 16), acc);
+            FAL_BWD_FENCE();
+          }
+          // fp32 atomics through a buffer resource that ends at row nq: rows past the end
+          // are dropped by the range check, offsets stay 32-bit
+          const int64_t rows_left = (int64_t)max(nq - qrb, 0);
+          const __amdgpu_buffer_rsrc_t qrs = make_rsrc(
+              qabase + (int64_t)qrb * p.dqa_ss + dq_db * 32,
+              (uint32_t)min(rows_left * p.dqa_ss * 4, (int64_t)0x7fffffff));
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = (i >> 2) * 8 + hh * 4 + (i & 3);
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(acc[i], qrs, (int)(r * p.dqa_ss + l32) * 4, 0, 0);
+          }
+        }
+      }
+    }
+
+    // ---- sum the two query halves' dK/dV and write this tile's rows ----
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(qd_s);   // [kg][32 keys][D] fp32
+    auto reduce_write = [&](f32x16 (&acc)[DWB], half_t* row, float sc) {
+      if (qh == 1) {
+#pragma unroll
+        for (int db = 0; db < DWB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            red[(kg * 32 + l32) * D + db * 32 + (i >> 2) * 8 + hh * 4 + (i & 3)] = acc[db][i];
+      }
+      __syncthreads();
+      if (qh == 0 && key < nk) {
+#pragma unroll
+        for (int db = 0; db < DWB; ++db)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int col = db * 32 + g4 * 8 + hh * 4;
+            const f32x4 o = *reinterpret_cast<const f32x4*>(&red[(kg * 32 + l32) * D + col]);
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)((acc[db][g4 * 4 + e] + o[e]) * sc);
+            *reinterpret_cast<half4*>(row + col) = h;
+          }
+      }
+      __syncthreads();
+    };
+    const int64_t krow = (int64_t)(k_off + min(key, max(nk - 1, 0)));
+    reduce_write(dk_acc, p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + krow * p.dk_ss, p.scale);
+    reduce_write(dv_acc, p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + krow * p.dv_ss, 1.f);
+  }
+}
+
 // --------------------------------------------------------------------------
 // Launchers
 // --------------------------------------------------------------------------
@@ -359,10 +671,19 @@ int bwd_block_n(int d) {
 
 template <int D>
 static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
-  if (causal)
-    hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, true>), grid, dim3(kBwdNW * 64), 0, st, p);
-  else
-    hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, false>), grid, dim3(kBwdNW * 64), 0, st, p);
+  if constexpr (D == 64 || D == 128) {
+    // batched causal: one workgroup per pair of key tiles
+    if (!p.cu_q && causal) grid.x = (unsigned)((p.n_ktiles + 1) / 2) * p.B * p.Hkv;
+    if (causal)
+      hipLaunchKernelGGL((bwd2_kernel<D, true>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((bwd2_kernel<D, false>), grid, dim3(512), 0, st, p);
+  } else {
+    if (causal)
+      hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, true>), grid, dim3(kBwdNW * 64), 0, st, p);
+    else
+      hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, false>), grid, dim3(kBwdNW * 64), 0, st, p);
+  }
   return hipGetLastError();
 }
 
