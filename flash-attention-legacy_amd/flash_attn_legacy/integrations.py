@@ -140,6 +140,19 @@ def flash_attn_legacy_forward(
     return attn_output, None
 
 
+def _config_head_dim_supported(config) -> bool:
+    """Head dim of a model config (``head_dim``, else ``hidden_size // num_attention_heads``)
+    is one the kernels support; unknown head dims count as supported (reference
+    integrations.py:146-154)."""
+    head_dim = getattr(config, "head_dim", None)
+    if head_dim is None:
+        hs = getattr(config, "hidden_size", None)
+        nh = getattr(config, "num_attention_heads", None)
+        if hs and nh:
+            head_dim = hs // nh
+    return head_dim is None or head_dim in _HEAD_DIMS
+
+
 def register():
     """Register flash_attn_legacy in transformers' attention registry (reference
     integrations.py:106-161).
@@ -162,13 +175,7 @@ def register():
 
         def _patched_check(self, attn_implementation, is_init_check=False, allow_all_kernels=False):
             if attn_implementation == "flash_attn_legacy":
-                head_dim = getattr(self.config, "head_dim", None)
-                if head_dim is None:
-                    hs = getattr(self.config, "hidden_size", None)
-                    nh = getattr(self.config, "num_attention_heads", None)
-                    if hs and nh:
-                        head_dim = hs // nh
-                if head_dim is not None and head_dim not in _HEAD_DIMS:
+                if not _config_head_dim_supported(self.config):
                     return original_check(self, "sdpa", is_init_check, allow_all_kernels)
                 return "flash_attn_legacy"
             return original_check(self, attn_implementation, is_init_check, allow_all_kernels)

@@ -1,0 +1,97 @@
+"""HuggingFace integration on the GPU with a tiny random LLaMA built offline (8 query
+heads, 2 KV heads, head_dim 64), after the reference's tests/test_transformers.py:38-162.
+attn_implementation="flash_attn_legacy" is compared with transformers' own "eager"
+attention on the same weights: prefill logits, one cached decode step (which runs
+the split-K decode kernel), generate, and gradients."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny_llama(impl):
+    import flash_attn_legacy  # noqa: F401  (registers the implementation)
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=256, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=512,
+                      rms_norm_eps=1e-5)
+    cfg._attn_implementation = impl
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).cuda().half()
+
+
+@pytest.fixture(scope="module")
+def models():
+    flash = tiny_llama("flash_attn_legacy")
+    eager = tiny_llama("eager")
+    eager.load_state_dict(flash.state_dict())
+    flash.eval()
+    eager.eval()
+    return flash, eager
+
+
+def cos(a, b):
+    return torch.nn.functional.cosine_similarity(a.float().reshape(1, -1), b.float().reshape(1, -1)).item()
+
+
+def test_prefill_logits_match_eager(models):
+    flash, eager = models
+    ids = torch.randint(0, 256, (2, 96), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
+    with torch.no_grad():
+        a = flash(ids).logits
+        b = eager(ids).logits
+    assert torch.isfinite(a).all()
+    assert cos(a, b) > 0.9999
+    assert (a.float() - b.float()).abs().max().item() < 0.05
+
+
+def test_cached_decode_step_uses_decode_kernel(models, monkeypatch):
+    from flash_attn_legacy import hip_ext
+    flash, eager = models
+    calls = []
+    real = hip_ext.decode
+    monkeypatch.setattr(hip_ext, "decode", lambda *a, **k: calls.append(1) or real(*a, **k))
+    ids = torch.randint(0, 256, (2, 40), device="cuda", generator=torch.Generator("cuda").manual_seed(2))
+    nxt = torch.randint(0, 256, (2, 1), device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    with torch.no_grad():
+        pa = flash(ids, use_cache=True)
+        la = flash(nxt, past_key_values=pa.past_key_values, use_cache=True).logits
+        pb = eager(ids, use_cache=True)
+        lb = eager(nxt, past_key_values=pb.past_key_values, use_cache=True).logits
+    assert len(calls) == 2          # one decode call per layer
+    assert cos(la, lb) > 0.9999
+    assert (la.float() - lb.float()).abs().max().item() < 0.05
+
+
+def test_generate(models):
+    flash, _ = models
+    ids = torch.randint(0, 256, (1, 8), device="cuda", generator=torch.Generator("cuda").manual_seed(4))
+    with torch.no_grad():
+        out = flash.generate(ids, max_new_tokens=16, do_sample=False)
+    assert out.shape[1] == 8 + 16
+
+
+@pytest.mark.parametrize("seq_len", [1, 16, 64, 128, 256])
+def test_different_seq_lengths(models, seq_len):
+    flash, _ = models
+    ids = torch.randint(0, 256, (1, seq_len), device="cuda")
+    with torch.no_grad():
+        out = flash(ids)
+    assert out.logits.shape == (1, seq_len, 256) and torch.isfinite(out.logits).all()
+
+
+def test_backward_matches_eager():
+    flash = tiny_llama("flash_attn_legacy")
+    eager = tiny_llama("eager")
+    eager.load_state_dict(flash.state_dict())
+    ids = torch.randint(0, 256, (1, 64), device="cuda", generator=torch.Generator("cuda").manual_seed(5))
+    la = flash(ids, labels=ids).loss
+    lb = eager(ids, labels=ids).loss
+    assert abs(la.item() - lb.item()) < 1e-2
+    la.backward()
+    lb.backward()
+    pa = dict(flash.named_parameters())
+    for name, p in eager.named_parameters():
+        if p.grad is not None and "self_attn" in name:
+            assert cos(pa[name].grad, p.grad) > 0.999, name
