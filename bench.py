@@ -127,7 +127,8 @@ def cpu_baseline(budget_s=15.0):
     over (batch, KV-group) slices of C2 -- 4 query heads x N=4096 x d=128, causal --
     until `budget_s` seconds have been spent.  Rate in TFLOP/s (same flop convention)."""
     from oracle.torch_ref import ref_attention
-    threads = os.cpu_count() or 1
+    # the GPU box grants one GPU's job 16 CPUs, whatever os.cpu_count() reports
+    threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
     B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
     gen = torch.Generator().manual_seed(0)
@@ -156,7 +157,7 @@ def cpu_baseline(budget_s=15.0):
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{done} of the 32 (batch, KV-group) slices of C2 (4 query heads x N=4096 x d=128, "
-                      f"causal), fp32 torch on CPU, {dt:.1f} s; os.cpu_count()={threads}; cpu={cpu_model}"}
+                      f"causal), fp32 torch on CPU, {dt:.1f} s; threads={threads}, os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
 
 
 def load_traffic():
@@ -175,7 +176,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c2", "all"], default="all")
+    ap.add_argument("--only", choices=["c2", "all", "copy"], default="all",
+                    help="c2: the headline line without the extra configurations; copy: a 1 GiB "
+                         "device copy only, the known-size kernel that calibrates HBM byte counters")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -184,6 +187,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+
+    if a.only == "copy":
+        src = torch.empty(1 << 29, dtype=torch.float16, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        wall, ev = time_steps(lambda: dst.copy_(src), a.steps, a.warmup)
+        print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
+                          "gbs": round(2 * src.numel() * 2 / ev / 1e6, 1)}), flush=True)
+        return
 
     wall, ev, flops = bench_c2(a.steps, a.warmup)
     value = flops / (wall * 1e-3) / 1e12

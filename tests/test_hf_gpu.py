@@ -95,3 +95,28 @@ def test_backward_matches_eager():
     for name, p in eager.named_parameters():
         if p.grad is not None and "self_attn" in name:
             assert cos(pa[name].grad, p.grad) > 0.999, name
+
+
+def test_llama_monkey_patch_example(models):
+    """examples/hf_llama_patch.py (reference examples/hf_llama_patch.py:18-130): the patched
+    model's prefill and cached decode logits match eager attention on the same weights."""
+    import importlib.util, os
+    path = os.path.join(os.path.dirname(__file__), "..", "flash-attention-legacy_amd", "examples", "hf_llama_patch.py")
+    spec = importlib.util.spec_from_file_location("hf_llama_patch", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    _, eager = models
+    patched = tiny_llama("eager")
+    patched.load_state_dict(eager.state_dict())
+    patched.eval()
+    mod.patch_llama_attention(patched)
+    ids = torch.randint(0, 256, (2, 50), device="cuda", generator=torch.Generator("cuda").manual_seed(6))
+    nxt = torch.randint(0, 256, (2, 1), device="cuda", generator=torch.Generator("cuda").manual_seed(7))
+    with torch.no_grad():
+        pa = patched(ids, use_cache=True)
+        pb = eager(ids, use_cache=True)
+        assert cos(pa.logits, pb.logits) > 0.9999
+        la = patched(nxt, past_key_values=pa.past_key_values, use_cache=True).logits
+        lb = eager(nxt, past_key_values=pb.past_key_values, use_cache=True).logits
+    assert cos(la, lb) > 0.9999
+    assert (la.float() - lb.float()).abs().max().item() < 0.05

@@ -214,3 +214,26 @@ def test_torch_fp32_reference_agrees_with_float64_oracle():
     gb = orc.attention_bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), 0.25, True)
     for x, y in zip(ga, gb):
         np.testing.assert_allclose(x.numpy(), y, atol=1e-4)
+
+
+def test_gqa_gradients_are_group_sums_of_mha_gradients():
+    """GQA backward == MHA backward on K/V repeated per group, with dK/dV summed over
+    the query heads of each group (the reference's in-block group loop,
+    csrc/kernels/flash_attn_bwd.cu:496)."""
+    hq, hkv, n, d = 6, 2, 7, 5
+    q, k, v, do = rnd(1, hq, n, d), rnd(1, hkv, n, d), rnd(1, hkv, n, d), rnd(1, hq, n, d)
+    g = hq // hkv
+    dq, dk, dv = orc.attention_bwd(q, k, v, do, 0.4, True)
+    mq, mk, mv = orc.attention_bwd(q, np.repeat(k, g, axis=1), np.repeat(v, g, axis=1), do, 0.4, True)
+    np.testing.assert_allclose(dq, mq, atol=1e-12)
+    np.testing.assert_allclose(dk, mk.reshape(1, hkv, g, n, d).sum(2), atol=1e-12)
+    np.testing.assert_allclose(dv, mv.reshape(1, hkv, g, n, d).sum(2), atol=1e-12)
+
+
+def test_decode_single_row_cache_returns_that_row():
+    """A cache of length 1 gives O = V[0] and L = q.k*scale, whatever q is."""
+    kc, vc, q = rnd(2, 5, 1, 4), rnd(2, 5, 1, 4), rnd(2, 1, 3, 4) * 10
+    o, lse = orc.decode(q, kc, vc, [1, 1], 0.7)
+    for b in range(2):
+        np.testing.assert_allclose(o[b, 0], np.repeat(vc[b, 0], 3, axis=0), atol=1e-12)
+        np.testing.assert_allclose(lse[b], q[b, 0] @ kc[b, 0, 0] * 0.7, atol=1e-12)
