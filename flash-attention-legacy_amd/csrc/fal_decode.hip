@@ -30,7 +30,7 @@ namespace fal {
 #define FAL_DEC_NW 4
 #endif
 #ifndef FAL_DEC_VAUX
-#define FAL_DEC_VAUX 0   // cache-policy bits of the V (LDS-direct) loads
+#define FAL_DEC_VAUX 2   // cache-policy bits of the V loads: nt (read once, evict first)
 #endif
 
 __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
@@ -269,20 +269,39 @@ decode_combine_kernel(DecodeParams p) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
   const float M_use = (M == -INFINITY) ? 0.f : M;
-  float acc[(D + 63) / 64];
+  constexpr int DJ = (D + 63) / 64;
+  float acc[DJ];
 #pragma unroll
-  for (int j = 0; j < (D + 63) / 64; ++j) acc[j] = 0.f;
+  for (int j = 0; j < DJ; ++j) acc[j] = 0.f;
   float wsum = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float wgt = fast_exp2(p.part_m[base + s] - M_use);
+  auto add_split = [&](float pm, const float* po) {
+    const float wgt = fast_exp2(pm - M_use);
     wsum += wgt;
-    const float* po = p.part_o + (base + s) * D;
 #pragma unroll
-    for (int j = 0; j < (D + 63) / 64; ++j) {
+    for (int j = 0; j < DJ; ++j) {
       const int d = lane + 64 * j;
       if (d < D) acc[j] = fmaf(wgt, po[d], acc[j]);
     }
+  };
+  int s = 0;
+  for (; s + 8 <= ns; s += 8) {   // eight splits' loads in flight per lane
+    float pm[8], x[8][DJ];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      pm[u] = p.part_m[base + s + u];
+      const float* po = p.part_o + (base + s + u) * D;
+#pragma unroll
+      for (int j = 0; j < DJ; ++j) x[u][j] = (lane + 64 * j < D) ? po[lane + 64 * j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float wgt = fast_exp2(pm[u] - M_use);
+      wsum += wgt;
+#pragma unroll
+      for (int j = 0; j < DJ; ++j) acc[j] = fmaf(wgt, x[u][j], acc[j]);
+    }
   }
+  for (; s < ns; ++s) add_split(p.part_m[base + s], p.part_o + (base + s) * D);
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   half_t* orow = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
 #pragma unroll
