@@ -197,9 +197,15 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
 // ---------------------------------------------------------------------------
 // Backward
 // ---------------------------------------------------------------------------
+// Backward workspace: delta [rows] fp32, plus, for head dims without the query-outer
+// dQ kernel, the fp32 dQ accumulator [rows, d] in front of it.
+static size_t bwd_acc_bytes(size_t rows, int64_t head_dim) {
+  return bwd_split_dq(head_dim_ok(head_dim) ? (int)head_dim : 0) ? 0 : align256(rows * head_dim * sizeof(float));
+}
+
 size_t fal_bwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t head_dim) {
   const size_t rows = (size_t)batch * heads_q * seqlen_q;
-  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+  return bwd_acc_bytes(rows, head_dim) + align256(rows * sizeof(float));
 }
 
 static int fill_bwd_common(BwdParams& p, const void* dout, const void* q, const void* k, const void* v,
@@ -234,12 +240,17 @@ static int fill_bwd_common(BwdParams& p, const void* dout, const void* q, const 
   return FAL_OK;
 }
 
-static int run_bwd(BwdParams& p, int d, int causal, dim3 grid, bool batched, hipStream_t st) {
+static int run_bwd(BwdParams& p, int d, int causal, dim3 grid, dim3 dq_grid, bool batched, hipStream_t st) {
   hipError_t e = launch_bwd_pre(p, d, batched ? 1 : 0, st);
   if (e != hipSuccess) return launch_status(e, "bwd preprocess");
   if (grid.x > 0 && grid.y > 0) {
     e = launch_bwd(p, d, causal, grid, st);
     if (e != hipSuccess) return launch_status(e, "bwd main");
+  }
+  if (bwd_split_dq(d)) {
+    if (dq_grid.x == 0 || dq_grid.y == 0) return ok();
+    e = launch_bwd_dq(p, d, causal, dq_grid, st);
+    return launch_status(e, "bwd dq");
   }
   e = launch_bwd_post(p, d, st);
   return launch_status(e, "bwd dq cast");
@@ -265,8 +276,9 @@ int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const
     return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
   if (batch == 0 || seqlen_k == 0 && seqlen_q == 0) return ok();
   const size_t rows = (size_t)batch * heads_q * seqlen_q;
-  p.dq_acc = static_cast<float*>(workspace);
-  p.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * head_dim * sizeof(float)));
+  const size_t acc = bwd_acc_bytes(rows, head_dim);
+  p.dq_acc = acc ? static_cast<float*>(workspace) : nullptr;
+  p.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
   p.dqa_sb = heads_q * seqlen_q * head_dim; p.dqa_sh = seqlen_q * head_dim; p.dqa_ss = head_dim;
   p.l_sb = heads_q * seqlen_q; p.l_sh = seqlen_q; p.l_ss = 1;
   p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
@@ -276,16 +288,25 @@ int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const
   const int bn = bwd_block_n((int)head_dim);
   p.n_ktiles = cdiv((int)seqlen_k, bn);
   const int64_t nblocks = (int64_t)p.n_ktiles * batch * heads_kv;
-  if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
-  return run_bwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), true, static_cast<hipStream_t>(stream));
+  const int64_t dq_blocks = (int64_t)cdiv((int)seqlen_q, bwd_dq_block_m((int)head_dim)) * batch * heads_q;
+  if (nblocks > 0x7fffffff || dq_blocks > 0x7fffffff)
+    return fail(FAL_ERR_INVALID, "problem too large for one launch");
+  return run_bwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), dim3((unsigned)dq_blocks), true,
+                 static_cast<hipStream_t>(stream));
 }
 
 size_t fal_bwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q,
                                      int64_t head_dim) {
   const size_t rows = (size_t)total_q * heads_q;
-  const int bn = bwd_block_n(head_dim_ok(head_dim) ? (int)head_dim : 128);
+  const int d = head_dim_ok(head_dim) ? (int)head_dim : 128;
+  const int bn = bwd_block_n(d);
   const size_t cap = (size_t)((total_k + bn - 1) / bn + num_seqs);
-  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) + align256(cap * sizeof(int2));
+  size_t bytes = bwd_acc_bytes(rows, head_dim) + align256(rows * sizeof(float)) + align256(cap * sizeof(int2));
+  if (bwd_split_dq(d)) {
+    const int bm = bwd_dq_block_m(d);
+    bytes += align256((size_t)((total_q + bm - 1) / bm + num_seqs) * sizeof(int2));
+  }
+  return bytes;
 }
 
 int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
@@ -296,7 +317,6 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
                    const int64_t* o_strides, const int64_t* dq_strides, const int64_t* dk_strides,
                    const int64_t* dv_strides, float softmax_scale, int is_causal, void* workspace,
                    size_t workspace_bytes, void* stream) {
-  (void)max_seqlen_q;
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
   if (num_seqs < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(total_q) || !dims_ok(total_k) ||
@@ -315,8 +335,9 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
   if (total_q == 0 && total_k == 0) return ok();
   const size_t rows = (size_t)total_q * heads_q;
   char* ws = static_cast<char*>(workspace);
-  p.dq_acc = reinterpret_cast<float*>(ws);
-  ws += align256(rows * head_dim * sizeof(float));
+  const size_t acc = bwd_acc_bytes(rows, head_dim);
+  p.dq_acc = acc ? reinterpret_cast<float*>(ws) : nullptr;
+  ws += acc;
   p.delta = reinterpret_cast<float*>(ws);
   ws += align256(rows * sizeof(float));
   int2* work = reinterpret_cast<int2*>(ws);
@@ -338,7 +359,20 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
   // segments are not written; the caller pre-zeroes dk/dv if it needs them defined.
   hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, bn, nb, 0, work, cap, st);
   if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen schedule");
-  return run_bwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_kv), false, st);
+  dim3 dq_grid(0, 0);
+  if (bwd_split_dq((int)head_dim)) {
+    // query tiles for the dQ kernel, longest first when causal
+    const int bm = bwd_dq_block_m((int)head_dim);
+    const int capq = (int)((total_q + bm - 1) / bm + num_seqs);
+    int2* qwork = work + align256((size_t)cap * sizeof(int2)) / sizeof(int2);
+    int nbq = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
+    nbq = nbq < 1 ? 1 : (nbq > 8192 ? 8192 : nbq);
+    e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, bm, nbq, is_causal ? 1 : 0, qwork, capq, st);
+    if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen dq schedule");
+    p.qwork = qwork;
+    dq_grid = dim3((unsigned)capq, (unsigned)heads_q);
+  }
+  return run_bwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_kv), dq_grid, false, st);
 }
 
 // ---------------------------------------------------------------------------

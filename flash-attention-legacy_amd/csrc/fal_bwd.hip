@@ -19,12 +19,15 @@
 //   transposed read) and adds it to the fp32 dQ accumulator with global atomics.
 // * For head_dim 256 the dK/dV accumulators are split into two passes over the
 //   query tiles (128 columns each); dQ is produced in the first pass.
+#include <type_traits>
+
 #include "fal_kernels.h"
 
 namespace fal {
 
 // --------------------------------------------------------------------------
-// Preprocess: delta = rowsum(dO * O) (fp32) and zero the fp32 dQ accumulator.
+// Preprocess: delta = rowsum(dO * O) (fp32) and zero the fp32 dQ accumulator when
+// the atomic dQ path is used.
 // One group of D/8 lanes per row (16-byte loads), reduced with xor shuffles.
 // --------------------------------------------------------------------------
 template <int D>
@@ -64,7 +67,7 @@ bwd_pre_kernel(BwdParams p, int rows, int batched) {
 #pragma unroll
   for (int off = G / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
   if (threadIdx.x % G == 0) p.delta[l_off] = s;
-  if (c >= D) return;
+  if (c >= D || !p.dq_acc) return;
   float* qa = p.dq_acc + qa_off + c;
   *reinterpret_cast<f32x4*>(qa) = f32x4{0.f, 0.f, 0.f, 0.f};
   *reinterpret_cast<f32x4*>(qa + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -376,7 +379,6 @@ template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(512)
 bwd2_kernel(BwdParams p) {
   using TL = SwizzledTile<D>;
-  using TS = SwizzledTile<64>;            // dS^T tile: 64 query columns per key row
   constexpr int NW = 8, BN = 128, BMQ = 64;
   constexpr int KS = D / 16;
   constexpr int DWB = D / 32;
@@ -391,7 +393,6 @@ bwd2_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(1024))) half_t ks_s[KPART];
   __shared__ __attribute__((aligned(1024))) half_t vs_s[KPART];
   __shared__ __attribute__((aligned(1024))) half_t qd_s[2 * 2 * QPART];   // [buffer][Q, dO]
-  __shared__ __attribute__((aligned(1024))) half_t dst_s[BN * BMQ];
   __shared__ float l_s[2][BMQ];
   __shared__ float d_s[2][BMQ];
 
@@ -451,7 +452,7 @@ bwd2_kernel(BwdParams p) {
   // tiles.  The swizzle is an XOR on the chunk index, so every address is a lane
   // base XOR a compile-time chunk offset; keeping only the bases saves registers.
   const int fbase = TL::offset(l32, hh);
-  int trb[2], sdb[2];
+  int trb[2];
   {
     const int i = lane & 15;
     const int rl = hh * 4 + (i >> 2);
@@ -459,7 +460,6 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       trb[hf] = TL::offset(hf * 8 + rl, cl);
-      sdb[hf] = TS::offset(hf * 8 + rl, qh * 4 + cl) + 4 * (lane & 1);
     }
   }
   const int tr_lo = 4 * (lane & 1);
@@ -470,14 +470,7 @@ bwd2_kernel(BwdParams p) {
     const half4 hi = lds_read_tr(base + (trb[1] ^ ((db * 4) << 3)) + tr_lo + row0 * CPR * 8);
     return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
-  auto trs = [&](int row0) {   // the same for the dS^T tile (64 columns, block qh)
-    const half4 lo = lds_read_tr(dst_s + sdb[0] + row0 * 64);
-    const half4 hi = lds_read_tr(dst_s + sdb[1] + row0 * 64);
-    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  };
-
   const int nqt = cdiv(nq, BMQ);
-  const int dq_db = w & 3;                // dQ block of this wave: rows qh*32.., cols dq_db*32..
 
   for (int tile_i = 0; tile_i < 2; ++tile_i) {
     const int kt = tile_i == 0 ? kt_a : kt_b;
@@ -505,52 +498,54 @@ bwd2_kernel(BwdParams p) {
       dv_acc[i] = zero_f16();
     }
     const int qt0 = CAUSAL ? (n0 / BMQ) : 0;
-
-    for (int g = 0; g < G; ++g) {
-      const int hq = hkv * G + g;
-      const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
-      const half_t* dobase = p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
-      const float* lbase = p.lse + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
-      const float* dbase_p = p.delta + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
-      float* qabase = p.dq_acc + (int64_t)b * p.dqa_sb + (int64_t)hq * p.dqa_sh + (int64_t)q_off * p.dqa_ss;
-
-      float lpre = 0.f, dpre = 0.f;
-      auto fetch = [&](int qt, int buf) {
-        const int q0 = qt * BMQ;
+    // (query head, query tile) items of this key tile, in one sequence so the Q/dO
+    // double buffer alternates across head boundaries too: the fetch of item it+1
+    // goes to the buffer item it-1 used, which every wave has finished with once it
+    // passes item it's barrier.
+    const int ntq = nqt > qt0 ? nqt - qt0 : 0;
+    const int nitems_q = G * ntq;
+    float lpre = 0.f, dpre = 0.f;
+    auto fetch = [&](int item, int buf) {
+      const int hq = hkv * G + item / ntq;
+      const int q0 = (qt0 + item % ntq) * BMQ;
+      const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)(q_off + q0) * p.q_ss;
+      const half_t* dobase =
+          p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)(q_off + q0) * p.do_ss;
 #pragma unroll
-        for (int i = 0; i < QIPT; ++i) {
-          const int I = i * NW + ws;
-          const int r0 = q0 + I * 64 / CPR;
-          const int64_t left = (int64_t)max(nq - r0, 0);
-          buffer_to_lds16(make_rsrc(qbase + (int64_t)r0 * p.q_ss, (uint32_t)min(left * p.q_ss * 2, (int64_t)0x7fffffff)),
-                          dl_offset(i, p.q_ss), qd_s + (buf * 2 + 0) * QPART + I * 64 * 8);
-          buffer_to_lds16(make_rsrc(dobase + (int64_t)r0 * p.do_ss, (uint32_t)min(left * p.do_ss * 2, (int64_t)0x7fffffff)),
-                          dl_offset(i, p.do_ss), qd_s + (buf * 2 + 1) * QPART + I * 64 * 8);
+      for (int i = 0; i < QIPT; ++i) {
+        const int I = i * NW + ws;
+        const int r0 = I * 64 / CPR;
+        const int64_t left = (int64_t)max(nq - q0 - r0, 0);
+        buffer_to_lds16(make_rsrc(qbase + (int64_t)r0 * p.q_ss, (uint32_t)min(left * p.q_ss * 2, (int64_t)0x7fffffff)),
+                        dl_offset(i, p.q_ss), qd_s + (buf * 2 + 0) * QPART + I * 64 * 8);
+        buffer_to_lds16(make_rsrc(dobase + (int64_t)r0 * p.do_ss, (uint32_t)min(left * p.do_ss * 2, (int64_t)0x7fffffff)),
+                        dl_offset(i, p.do_ss), qd_s + (buf * 2 + 1) * QPART + I * 64 * 8);
+      }
+      if (tid < BMQ) {
+        float lv = INFINITY, dv = 0.f;
+        if (q0 + tid < nq) {
+          const int64_t o = (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)(q_off + q0 + tid) * p.l_ss;
+          const float L = p.lse[o];
+          lv = (L == -INFINITY) ? INFINITY : L * kLog2e;
+          dv = p.delta[o];
         }
-        if (tid < BMQ) {
-          float lv = INFINITY, dv = 0.f;
-          if (q0 + tid < nq) {
-            const int o = tid * (int)p.l_ss;
-            const float L = (lbase + (int64_t)q0 * p.l_ss)[o];
-            lv = (L == -INFINITY) ? INFINITY : L * kLog2e;
-            dv = (dbase_p + (int64_t)q0 * p.l_ss)[o];
-          }
-          lpre = lv;
-          dpre = dv;
-        }
-      };
+        lpre = lv;
+        dpre = dv;
+      }
+    };
 
-      if (qt0 < nqt) fetch(qt0, 0);
-      for (int qt = qt0; qt < nqt; ++qt) {
-        const int buf = (qt - qt0) & 1;
-        const int q0 = qt * BMQ;
+    if (nitems_q > 0) fetch(0, 0);
+    for (int item = 0; item < nitems_q; ++item) {
+      {
+        const int buf = item & 1;
+        const int q0 = (qt0 + item % ntq) * BMQ;
         wait_vmcnt0();
         if (tid < BMQ) {
           l_s[buf][tid] = lpre;
           d_s[buf][tid] = dpre;
         }
-        __syncthreads();                  // barrier A: tile qt in LDS; dQ readers of qt-1 done
-        if (qt + 1 < nqt) fetch(qt + 1, buf ^ 1);
+        __syncthreads();                  // barrier A: item in LDS; readers of item-1 done
+        if (item + 1 < nitems_q) fetch(item + 1, buf ^ 1);
         const half_t* q_s = qd_s + (buf * 2 + 0) * QPART + qh * 32 * CPR * 8;
         const half_t* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
         const int qr0 = q0 + qh * 32;     // first query row of this wave's half
@@ -591,37 +586,6 @@ bwd2_kernel(BwdParams p) {
               FAL_BWD_FENCE();
             }
           }
-          // dS^T (fp16) into LDS: row = key (tile-local), 64 query columns
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            half4 h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)dp[g4 * 4 + e];
-            const int col = qh * 32 + g4 * 8 + hh * 4;
-            *reinterpret_cast<half4*>(dst_s + TS::offset(kg * 32 + l32, col >> 3) + (col & 7)) = h;
-          }
-        }
-        __syncthreads();                  // barrier B: dS^T complete
-        // dQ[q0 + qh*32 .. +32, dq_db*32 .. +32] += dS K over the active key steps
-        if (dq_db < DWB) {
-          const int qrb = q0 + qh * 32;
-          f32x16 acc = zero_f16();
-          for (int ks = 0; ks < BN / 16; ++ks) {
-            if (CAUSAL && qrb + 31 < n0 + (ks >> 1) * 32) break;
-            acc = mfma32(trs(ks * 16), trk(ks_s, dq_db, ks * 16), acc);
-            FAL_BWD_FENCE();
-          }
-          // fp32 atomics through a buffer resource that ends at row nq: rows past the end
-          // are dropped by the range check, offsets stay 32-bit
-          const int64_t rows_left = (int64_t)max(nq - qrb, 0);
-          const __amdgpu_buffer_rsrc_t qrs = make_rsrc(
-              qabase + (int64_t)qrb * p.dqa_ss + dq_db * 32,
-              (uint32_t)min(rows_left * p.dqa_ss * 4, (int64_t)0x7fffffff));
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int r = (i >> 2) * 8 + hh * 4 + (i & 3);
-            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(acc[i], qrs, (int)(r * p.dqa_ss + l32) * 4, 0, 0);
-          }
         }
       }
     }
@@ -659,6 +623,247 @@ bwd2_kernel(BwdParams p) {
   }
 }
 
+
+// --------------------------------------------------------------------------
+// Query-outer dQ kernel for head_dim 64 and 128 (the KV-outer kernel above then
+// produces only dK/dV).  Same structure as the forward kernel: a workgroup owns
+// 32*NW query rows of one query head, each wave 32 rows whose Q and dO slices stay
+// in VGPRs as the B operands of S^T = K Q^T and dP^T = V dO^T; K/V tiles of BN keys
+// are staged in swizzled LDS by direct buffer loads, double-buffered.  Per tile:
+// P^T = exp2(S^T * scale*log2e - L*log2e), dS^T = P^T (dP^T - D), and
+// dQ^T += K^T dS^T with dS^T taken straight from the accumulator as the B operand
+// and K^T read transposed from the K tile.  dQ is written once, in fp16, scaled:
+// no fp32 accumulator and no atomics.
+// --------------------------------------------------------------------------
+template <int D, int NW, int BN, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
+bwd_dq_kernel(BwdParams p) {
+  using TL = SwizzledTile<D>;
+  constexpr int BM = NW * 32;
+  constexpr int KS = D / 16;
+  constexpr int NKB = BN / 32;
+  constexpr int DB = D / 32;
+  constexpr int CPR = TL::CPR;
+  constexpr int PART = BN * CPR * 8;
+  constexpr int IPT = BN * CPR / (NW * 64);
+  static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
+
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * 2 * PART];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  int b, hq, qt, q_off, k_off, nq, nk;
+  if (p.cu_q) {
+    const int2 wk = p.qwork[blockIdx.x];
+    if (wk.x < 0) return;
+    hq = blockIdx.y;
+    b = 0;
+    qt = wk.y;
+    q_off = p.cu_q[wk.x];
+    nq = p.cu_q[wk.x + 1] - q_off;
+    k_off = p.cu_k[wk.x];
+    nk = p.cu_k[wk.x + 1] - k_off;
+  } else {
+    // heads of one KV head and the query tiles of a head are dealt to one XCD together
+    const int total = gridDim.x;
+    int id = blockIdx.x;
+    if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+    const int nqt = cdiv(p.Nq, BM);
+    const int g = p.Hq / p.Hkv;
+    const int hg = id % g;
+    int rest = id / g;
+    const int t = rest % nqt;
+    rest /= nqt;
+    qt = CAUSAL ? (nqt - 1 - t) : t;
+    b = rest / p.Hkv;
+    hq = (rest % p.Hkv) * g + hg;
+    q_off = 0;
+    k_off = 0;
+    nq = p.Nq;
+    nk = p.Nk;
+  }
+  const int hkv = hq / (p.Hq / p.Hkv);
+  const int m0 = qt * BM;
+  if (m0 >= nq) return;
+
+  const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
+  const half_t* dobase = p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
+  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
+  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
+  const int64_t lrow = (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
+
+  // Q and dO slices of this wave (B operands: n = query row, k = head dim), and the
+  // row's log-sum-exp (log2 domain) and delta
+  const int row = m0 + w * 32 + l32;
+  half8 qreg[KS], doreg[KS];
+  float lrow2 = INFINITY, drow = 0.f;
+  if (row < nq) {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      qreg[t] = load_h8(qbase + (int64_t)row * p.q_ss + t * 16 + hh * 8);
+      doreg[t] = load_h8(dobase + (int64_t)row * p.do_ss + t * 16 + hh * 8);
+    }
+    const float L = p.lse[lrow + (int64_t)row * p.l_ss];
+    lrow2 = (L == -INFINITY) ? INFINITY : L * kLog2e;
+    drow = p.delta[lrow + (int64_t)row * p.l_ss];
+  } else {
+#pragma unroll
+    for (int t = 0; t < KS; ++t) qreg[t] = doreg[t] = zero_h8();
+  }
+  const float c = p.scale_log2;
+
+  const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
+  const int ntiles = cdiv(kend, BN);
+  const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
+
+  const int ws = __builtin_amdgcn_readfirstlane(w);
+  int kvo[IPT], vvo[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int I = i * NW + ws;
+    const int row0 = I * 64 / CPR;
+    const int pch = I * 64 + lane;
+    const int r = pch / CPR;
+    const int cc = TL::logical_chunk(r, pch % CPR);
+    kvo[i] = (int)((r - row0) * p.k_ss + cc * 8) * 2;
+    vvo[i] = (int)((r - row0) * p.v_ss + cc * 8) * 2;
+  }
+  int kaddr[KS];   // fragment (row l32, chunk 2t+hh) of 32-key block 0
+#pragma unroll
+  for (int t = 0; t < KS; ++t) kaddr[t] = TL::offset(l32, 2 * t + hh);
+  int taddr[2][DB];   // transposed reads: rows hf*8 + hh*4 + i/4 of each 16-key step
+  {
+    const int i = lane & 15;
+    const int rl = hh * 4 + (i >> 2);
+    const int cl = 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) taddr[hf][db] = TL::offset(hf * 8 + rl, db * 4 + cl) + 4 * (lane & 1);
+  }
+
+  auto load_tile = [&](int tile, int buf) {
+    const int n0 = tile * BN;
+    half_t* kdst = smem + buf * 2 * PART;
+    half_t* vdst = kdst + PART;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      const int I = i * NW + ws;
+      const int r0 = n0 + I * 64 / CPR;
+      const int64_t left = (int64_t)max(nk - r0, 0);
+      const uint32_t kb = (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff);
+      const uint32_t vb = (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff);
+      buffer_to_lds16(make_rsrc(kbase + (int64_t)r0 * p.k_ss, kb), kvo[i], kdst + I * 64 * 8);
+      buffer_to_lds16(make_rsrc(vbase + (int64_t)r0 * p.v_ss, vb), vvo[i], vdst + I * 64 * 8);
+    }
+  };
+
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) dqacc[i] = zero_f16();
+
+  auto tile_body = [&](auto masked, int j, int buf) {
+    constexpr bool MASK = decltype(masked)::value;
+    const int n0 = j * BN;
+    const half_t* ks = smem + buf * 2 * PART;
+    const half_t* vs = ks + PART;
+    // S^T = K Q^T and dP^T = V dO^T; fragments read one k-step ahead of their MFMAs
+    f32x16 sacc[NKB], pacc[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) sacc[kb] = pacc[kb] = zero_f16();
+    half8 kf[2][NKB], vf[2][NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      kf[0][kb] = load_h8(ks + kaddr[0] + kb * 32 * CPR * 8);
+      vf[0][kb] = load_h8(vs + kaddr[0] + kb * 32 * CPR * 8);
+    }
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      if (t + 1 < KS) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          kf[(t + 1) & 1][kb] = load_h8(ks + kaddr[t + 1] + kb * 32 * CPR * 8);
+          vf[(t + 1) & 1][kb] = load_h8(vs + kaddr[t + 1] + kb * 32 * CPR * 8);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NKB, 0);
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        sacc[kb] = mfma32(kf[t & 1][kb], qreg[t], sacc[kb]);
+        pacc[kb] = mfma32(vf[t & 1][kb], doreg[t], pacc[kb]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * NKB, 0);
+    }
+    // P^T and dS^T; element i: key n0 + kb*32 + (i/4)*8 + hh*4 + i%4, query `row`
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float pv = fast_exp2(fmaf(sacc[kb][i], c, -lrow2));
+        if (MASK) {
+          const int key = n0 + kb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+          if (key >= nk || (CAUSAL && key > row)) pv = 0.f;
+        }
+        pacc[kb][i] = pv * (pacc[kb][i] - drow);
+      }
+    // dQ^T += K^T dS^T
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const half8 sb = cvt8(pacc[kb], t2);
+        const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const half4 lo = lds_read_tr(ks + taddr[0][db] + kofs);
+          const half4 hi = lds_read_tr(ks + taddr[1][db] + kofs);
+          dqacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, sb, dqacc[db]);
+        }
+      }
+  };
+  auto step = [&](auto masked, int j, int buf) {
+    wait_vmcnt0();
+    __syncthreads();
+    if (j + 1 < ntiles) load_tile(j + 1, buf ^ 1);
+    tile_body(masked, j, buf);
+  };
+
+  if (ntiles > 0) load_tile(0, 0);
+  int j = 0;
+  for (; j + 1 < nfull; j += 2) {
+    step(std::false_type{}, j, 0);
+    step(std::false_type{}, j + 1, 1);
+  }
+  if (j < nfull) {
+    step(std::false_type{}, j, 0);
+    ++j;
+  }
+  const int wrow_hi = m0 + w * 32 + 31;
+  for (; j < ntiles; ++j) {
+    wait_vmcnt0();
+    __syncthreads();
+    if (j + 1 < ntiles) load_tile(j + 1, (j + 1) & 1);
+    if (!CAUSAL || j * BN <= wrow_hi) tile_body(std::true_type{}, j, j & 1);
+  }
+
+  if (row < nq) {
+    half_t* dqrow = p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)(q_off + row) * p.dq_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = (half_t)(dqacc[db][g4 * 4 + e] * p.scale);
+        *reinterpret_cast<half4*>(dqrow + db * 32 + g4 * 8 + hh * 4) = h;
+      }
+  }
+}
+
 // --------------------------------------------------------------------------
 // Launchers
 // --------------------------------------------------------------------------
@@ -685,6 +890,34 @@ static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStr
       hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, false>), grid, dim3(kBwdNW * 64), 0, st, p);
   }
   return hipGetLastError();
+}
+
+#ifndef FAL_BWD_DQ_BN
+#define FAL_BWD_DQ_BN 64
+#endif
+constexpr int kDqNW = 4;
+
+bool bwd_split_dq(int d) { return d == 64 || d == 128; }
+int bwd_dq_block_m(int d) {
+  (void)d;
+  return kDqNW * 32;
+}
+
+template <int D>
+static hipError_t launch_bwd_dq_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+  if (causal)
+    hipLaunchKernelGGL((bwd_dq_kernel<D, kDqNW, FAL_BWD_DQ_BN, true>), grid, dim3(kDqNW * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL((bwd_dq_kernel<D, kDqNW, FAL_BWD_DQ_BN, false>), grid, dim3(kDqNW * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st) {
+  switch (d) {
+    case 64: return launch_bwd_dq_d<64>(p, causal, grid, st);
+    case 128: return launch_bwd_dq_d<128>(p, causal, grid, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_bwd(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st) {

@@ -63,6 +63,7 @@ struct BwdParams {
   const int* cu_q;
   const int* cu_k;
   const int2* work;   // (sequence, kv-tile) list in varlen mode
+  const int2* qwork;  // (sequence, query-tile) list of the dQ kernel in varlen mode
   int total_q;        // varlen: rows of the packed Q (row-wise kernels)
 };
 
@@ -97,6 +98,10 @@ int bwd_block_n(int d);
 hipError_t launch_bwd(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 hipError_t launch_bwd_pre(const BwdParams& p, int d, int rows_batched, hipStream_t st);
 hipError_t launch_bwd_post(const BwdParams& p, int d, hipStream_t st);
+// head dims whose dQ comes from the query-outer kernel (no fp32 accumulator)
+bool bwd_split_dq(int d);
+int bwd_dq_block_m(int d);
+hipError_t launch_bwd_dq(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 
 int decode_chunk(int d, int B, int Hkv, int max_seqlen);
 hipError_t launch_decode(const DecodeParams& p, int d, hipStream_t st);
