@@ -635,8 +635,14 @@ bwd2_kernel(BwdParams p) {
 // and K^T read transposed from the K tile.  dQ is written once, in fp16, scaled:
 // no fp32 accumulator and no atomics.
 // --------------------------------------------------------------------------
+#ifndef FAL_BWD_DQ_PAIR
+#define FAL_BWD_DQ_PAIR 1
+#endif
+#ifndef FAL_BWD_DQ_WPE
+#define FAL_BWD_DQ_WPE 2
+#endif
 template <int D, int NW, int BN, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(FAL_BWD_DQ_WPE, 8)))
 bwd_dq_kernel(BwdParams p) {
   using TL = SwizzledTile<D>;
   constexpr int BM = NW * 32;
@@ -656,13 +662,13 @@ bwd_dq_kernel(BwdParams p) {
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
-  int b, hq, qt, q_off, k_off, nq, nk;
+  int b, hq, qt_a, qt_b = -1, q_off, k_off, nq, nk;
   if (p.cu_q) {
     const int2 wk = p.qwork[blockIdx.x];
     if (wk.x < 0) return;
     hq = blockIdx.y;
     b = 0;
-    qt = wk.y;
+    qt_a = wk.y;
     q_off = p.cu_q[wk.x];
     nq = p.cu_q[wk.x + 1] - q_off;
     k_off = p.cu_k[wk.x];
@@ -672,13 +678,16 @@ bwd_dq_kernel(BwdParams p) {
     const int total = gridDim.x;
     int id = blockIdx.x;
     if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+    // causal: a workgroup takes query tiles t and nqt-1-t, so all do equal work
     const int nqt = cdiv(p.Nq, BM);
+    const int nitems = (CAUSAL && FAL_BWD_DQ_PAIR) ? (nqt + 1) / 2 : nqt;
     const int g = p.Hq / p.Hkv;
     const int hg = id % g;
     int rest = id / g;
-    const int t = rest % nqt;
-    rest /= nqt;
-    qt = CAUSAL ? (nqt - 1 - t) : t;
+    const int t = rest % nitems;
+    rest /= nitems;
+    qt_a = CAUSAL ? (nqt - 1 - t) : t;
+    if (CAUSAL && FAL_BWD_DQ_PAIR && t != nqt - 1 - t) qt_b = t;
     b = rest / p.Hkv;
     hq = (rest % p.Hkv) * g + hg;
     q_off = 0;
@@ -687,8 +696,12 @@ bwd_dq_kernel(BwdParams p) {
     nk = p.Nk;
   }
   const int hkv = hq / (p.Hq / p.Hkv);
+  for (int pass = 0; pass < 2; ++pass) {
+  const int qt = pass == 0 ? qt_a : qt_b;
+  if (qt < 0) break;
+  if (pass) __syncthreads();   // the previous tile's LDS readers are done
   const int m0 = qt * BM;
-  if (m0 >= nq) return;
+  if (m0 >= nq) continue;
 
   const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
   const half_t* dobase = p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
@@ -862,6 +875,7 @@ bwd_dq_kernel(BwdParams p) {
         *reinterpret_cast<half4*>(dqrow + db * 32 + g4 * 8 + hh * 4) = h;
       }
   }
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -905,6 +919,8 @@ int bwd_dq_block_m(int d) {
 
 template <int D>
 static hipError_t launch_bwd_dq_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+  if (!p.cu_q && causal && FAL_BWD_DQ_PAIR)
+    grid.x = (unsigned)((cdiv(p.Nq, kDqNW * 32) + 1) / 2) * p.B * p.Hq;
   if (causal)
     hipLaunchKernelGGL((bwd_dq_kernel<D, kDqNW, FAL_BWD_DQ_BN, true>), grid, dim3(kDqNW * 64), 0, st, p);
   else
