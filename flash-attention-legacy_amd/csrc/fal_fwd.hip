@@ -24,35 +24,23 @@
 namespace fal {
 
 // Tunables (compile-time): minimum waves per SIMD the register budget must allow,
-// KV tile width for head_dim <= 128, lazy-rescale threshold (log2 units).
+// KV tile width for head_dim <= 128, K fragment read-ahead (k-steps).
 #ifndef FAL_FWD_WPE
 #define FAL_FWD_WPE 2
 #endif
 #ifndef FAL_FWD_BN
 #define FAL_FWD_BN 64
 #endif
-#ifndef FAL_FWD_ABLATE
-#define FAL_FWD_ABLATE 0
-#endif
 #ifndef FAL_FWD_KDEPTH
 #define FAL_FWD_KDEPTH 2
 #endif
-#if FAL_FWD_SETPRIO
-#define FAL_PRIO_MFMA() __builtin_amdgcn_s_setprio(1)
-#define FAL_PRIO_VALU() __builtin_amdgcn_s_setprio(0)
-#else
-#define FAL_PRIO_MFMA() ((void)0)
-#define FAL_PRIO_VALU() ((void)0)
-#endif
-#ifndef FAL_FWD_RESCALE_THRESHOLD
-#define FAL_FWD_RESCALE_THRESHOLD 8.0f
-#endif
 
-template <int D, int NW, int BN, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? FAL_FWD_WPE : 1, 8)))
+template <int D, int NW, int BN, bool CAUSAL, int RB>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(RB == 2 ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
 fwd_kernel(FwdParams p) {
   using TL = SwizzledTile<D>;
-  constexpr int BM = NW * 32;
+  constexpr int BM = NW * 32 * RB;  // query rows per workgroup (RB 32-row blocks per wave)
   constexpr int KS = D / 16;        // MFMA k-steps over the head dim
   constexpr int NKB = BN / 32;      // 32-key blocks per tile
   constexpr int DB = D / 32;        // 32-wide blocks of the output head dim
@@ -111,13 +99,24 @@ fwd_kernel(FwdParams p) {
   half_t* obase = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)q_off * p.o_ss;
   float* lbase = p.lse + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
 
-  // ---- Q slice of this wave into registers (B operand: n = query row, k = head dim) ----
-  const int row = m0 + w * 32 + l32;
-  half8 qreg[KS];
+  // ---- Q slices of this wave into registers (B operand: n = query row, k = head dim) ----
+  // Row block rb of wave w covers rows m0 + (w*RB + rb)*32 ..; each K or V fragment read
+  // from LDS feeds RB MFMAs.  Q is pre-multiplied by c = softmax_scale * log2(e) (the
+  // sign included), so the MFMA yields scores in the log2 domain directly.
+  const float c = p.scale_log2;
+  int row[RB];
+  half8 qreg[RB][KS];
 #pragma unroll
-  for (int t = 0; t < KS; ++t)
-    qreg[t] = row < nq ? load_h8(qbase + (int64_t)row * p.q_ss + t * 16 + hh * 8) : zero_h8();
-  const float c = p.scale_log2;   // softmax_scale * log2(e), signed
+  for (int rb = 0; rb < RB; ++rb) {
+    row[rb] = m0 + (w * RB + rb) * 32 + l32;
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      half8 x = row[rb] < nq ? load_h8(qbase + (int64_t)row[rb] * p.q_ss + t * 16 + hh * 8) : zero_h8();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (half_t)((float)x[e] * c);
+      qreg[rb][t] = x;
+    }
+  }
 
   // ---- key range ----
   const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
@@ -139,9 +138,9 @@ fwd_kernel(FwdParams p) {
     const int row0 = I * 64 / CPR;
     const int pch = I * 64 + lane;
     const int r = pch / CPR;
-    const int c = TL::logical_chunk(r, pch % CPR);
-    kvo[i] = (int)((r - row0) * p.k_ss + c * 8) * 2;
-    vvo[i] = (int)((r - row0) * p.v_ss + c * 8) * 2;
+    const int cc = TL::logical_chunk(r, pch % CPR);
+    kvo[i] = (int)((r - row0) * p.k_ss + cc * 8) * 2;
+    vvo[i] = (int)((r - row0) * p.v_ss + cc * 8) * 2;
   }
   int kaddr[KS];                     // K fragment (row l32, chunk 2t+hh) for 32-key block 0
 #pragma unroll
@@ -174,13 +173,23 @@ fwd_kernel(FwdParams p) {
     }
   };
 
-  f32x16 oacc[DB];
+  f32x16 oacc[RB][DB];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) oacc[i] = zero_f16();
-  float m_run = -INFINITY;   // running max, log2 domain (may lag the true max by < threshold)
-  float l_run = 0.f;         // running sum of this lane's keys
-  const bool pos = c >= 0.f;
-  const float mval = pos ? -INFINITY : INFINITY;   // masked raw score
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int i = 0; i < DB; ++i) oacc[rb][i] = zero_f16();
+  // m_run: reference max of the row (log2 domain); it may lag the true running max, as
+  // long as every p = exp2(s - m_run) of a tile fits fp16 (the tile's p sum <= 2^15).
+  // negm: -m_run broadcast over an accumulator block, the starting value of S^T, so the
+  // MFMAs produce s - m_run without a VALU pass.
+  float m_run[RB], l_run[RB];
+  f32x16 negm[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
+    negm[rb] = zero_f16();
+  }
 
   auto tile_body = [&](auto masked, int j, int buf) {
     constexpr bool MASK = decltype(masked)::value;
@@ -189,9 +198,7 @@ fwd_kernel(FwdParams p) {
     const half_t* vs = ks + PART;
     // S^T = K Q^T, the 32-key blocks interleaved so consecutive MFMAs are independent.
     // K fragments are read FAL_FWD_KDEPTH k-steps ahead of the MFMAs that use them.
-    f32x16 sacc[NKB];
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) sacc[kb] = zero_f16();
+    f32x16 sacc[RB][NKB];
     half8 kfrag[KS][NKB];
 #pragma unroll
     for (int t = 0; t < FAL_FWD_KDEPTH && t < KS; ++t)
@@ -206,101 +213,105 @@ fwd_kernel(FwdParams p) {
           kfrag[t + FAL_FWD_KDEPTH][kb] = load_h8(ks + kaddr[t + FAL_FWD_KDEPTH] + kb * 32 * CPR * 8);
         __builtin_amdgcn_sched_group_barrier(0x100, NKB, 0);   // the reads ...
       }
-      FAL_PRIO_MFMA();
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) sacc[kb] = mfma32(kfrag[t][kb], qreg[t], sacc[kb]);
-      __builtin_amdgcn_sched_group_barrier(0x008, NKB, 0);     // ... then the MFMAs of step t
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          sacc[rb][kb] = mfma32(kfrag[t][kb], qreg[rb][t], t == 0 ? negm[rb] : sacc[rb][kb]);
+      __builtin_amdgcn_sched_group_barrier(0x008, NKB * RB, 0);  // ... then the MFMAs of step t
     }
-    FAL_PRIO_VALU();
     if (MASK) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = n0 + kb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
-          if (key >= nk || (CAUSAL && key > row)) sacc[kb][i] = mval;
-        }
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = n0 + kb * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+            if (key >= nk || (CAUSAL && key > row[rb])) sacc[rb][kb][i] = -INFINITY;
+          }
     }
-#if FAL_FWD_ABLATE == 1
+    // P^T = exp2(s - m_run) in fp16 (the B operand of O^T += V^T P^T) and this tile's
+    // per-lane p sum
+    half8 pb[RB][NKB][2];
+    float lt[RB];
+    auto make_p = [&]() {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        lt[rb] = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) {
+            half8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (half_t)fast_exp2(sacc[rb][kb][t2 * 8 + e]);
+            pb[rb][kb][t2] = h;
+            lt[rb] = sum8_f16(h, lt[rb]);
+          }
+      }
+    };
+    make_p();
+    // The reference max moves only when some p of the tile could leave fp16 range
+    // (or on a row's first keys): then rescale O and l to the tile's true max.
+    bool fix = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) fix |= !(lt[rb] <= 32768.f) || m_run[rb] == -INFINITY;
+    if (__builtin_amdgcn_ballot_w64(fix)) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[rb][kb][i]);
+        mx = pair_max(mx);
+        // scores are s - m_use, m_use = (m_run == -inf ? 0 : m_run)
+        const bool first = m_run[rb] == -INFINITY;
+        const float dlt = (mx == -INFINITY) ? 0.f : (first ? mx : fmaxf(mx, 0.f));
+        if (first) {
+          if (mx != -INFINITY) m_run[rb] = mx;
+        } else {
+          m_run[rb] += dlt;
+          const float alpha = fast_exp2(-dlt);
+          l_run[rb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[rb][db][i] *= alpha;
+        }
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[rb][kb][i] -= dlt;
+        const float nm = (m_run[rb] == -INFINITY) ? 0.f : -m_run[rb];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) negm[rb][i] = nm;
+      }
+      make_p();
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) l_run[rb] += lt[rb];
+#pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
-        const half8 pb = cvt8(sacc[kb], t2);
         const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
+#pragma unroll
         for (int db = 0; db < DB; ++db) {
           const half4 lo = lds_read_tr(vs + vaddr[0][db] + kofs);
           const half4 hi = lds_read_tr(vs + vaddr[1][db] + kofs);
-          oacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
+          const half8 va = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) oacc[rb][db] = mfma32(va, pb[rb][kb][t2], oacc[rb][db]);
         }
       }
-    return;
-#endif
-    // row max of scale*s (scale may be negative: reduce with min then)
-    float mx;
-    if (pos) {
-      mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb][i]);
-      mx = pair_max(mx);
-    } else {
-      mx = INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fminf(mx, sacc[kb][i]);
-      mx = -pair_max(-mx);
-    }
-    const float m_new = fmaxf(m_run, mx * c);
-    // Lazy rescale: move the reference max only when it grew by more than the
-    // threshold somewhere in the wave, so p stays <= 2^threshold and the O/l
-    // rescale runs on few tiles.
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run + FAL_FWD_RESCALE_THRESHOLD)) {
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-    // P^T = exp2(s*c - m), straight into the B operand of O^T += V^T P^T
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[kb][i] = fast_exp2(fmaf(sacc[kb][i], c, -m_use));
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        const half8 pb = cvt8(sacc[kb], t2);
-        l_run = sum8_f16(pb, l_run);
-        const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
-#if FAL_FWD_ABLATE == 2
-        oacc[0][0] += (float)pb[0] + (float)pb[7];
-        (void)kofs;
-#else
-        FAL_PRIO_MFMA();
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const half4 lo = lds_read_tr(vs + vaddr[0][db] + kofs);
-          const half4 hi = lds_read_tr(vs + vaddr[1][db] + kofs);
-          oacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
-        }
-#endif
-      }
-    FAL_PRIO_VALU();
   };
   // One pipeline step: wait for tile j, prefetch tile j+1 into the other buffer, consume j.
   auto step = [&](auto masked, int j, int buf) {
-#if FAL_FWD_ABLATE != 4
     wait_vmcnt0();
     __syncthreads();                       // tile j visible; tile j-1 reads finished
-#endif
-#if FAL_FWD_ABLATE != 3
     if (j + 1 < ntiles) load_tile(j + 1, buf ^ 1);
-#endif
     tile_body(masked, j, buf);
   };
 
@@ -318,7 +329,7 @@ fwd_kernel(FwdParams p) {
   }
   // Diagonal and tail tiles; waves whose rows all precede the tile only keep the
   // pipeline (barrier + prefetch) going.
-  const int wrow_hi = m0 + w * 32 + 31;   // last query row of this wave
+  const int wrow_hi = m0 + (w * RB + RB - 1) * 32 + 31;   // last query row of this wave
   for (; j < ntiles; ++j) {
     wait_vmcnt0();
     __syncthreads();
@@ -327,23 +338,26 @@ fwd_kernel(FwdParams p) {
   }
 
   // ---- epilogue: normalise, write O and L ----
-  const float l_tot = pair_sum(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (row < nq) {
-    half_t* orow = obase + (int64_t)row * p.o_ss;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+  for (int rb = 0; rb < RB; ++rb) {
+    const float l_tot = pair_sum(l_run[rb]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (row[rb] < nq) {
+      half_t* orow = obase + (int64_t)row[rb] * p.o_ss;
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        half4 h;
+      for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (half_t)(oacc[db][g4 * 4 + e] * inv);
-        *reinterpret_cast<half4*>(orow + db * 32 + g4 * 8 + hh * 4) = h;
+        for (int g4 = 0; g4 < 4; ++g4) {
+          half4 h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (half_t)(oacc[rb][db][g4 * 4 + e] * inv);
+          *reinterpret_cast<half4*>(orow + db * 32 + g4 * 8 + hh * 4) = h;
+        }
+      if (hh == 0) {
+        float L = -INFINITY;
+        if (l_tot > 0.f) L = (m_run[rb] + fast_log2(l_tot)) * kLn2;
+        lbase[(int64_t)row[rb] * p.l_ss] = L;
       }
-    if (hh == 0) {
-      float L = -INFINITY;
-      if (l_tot > 0.f) L = (m_run + fast_log2(l_tot)) * kLn2;
-      lbase[(int64_t)row * p.l_ss] = L;
     }
   }
 }
@@ -393,25 +407,31 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int tile, int n
 // ---------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------
+#ifndef FAL_FWD_RB128
+#define FAL_FWD_RB128 1   // 32-row blocks per wave for head_dim 128
+#endif
 template <int D>
 struct FwdCfg {
   static constexpr int NW = 4;
   static constexpr int BN = (D >= 256) ? 32 : FAL_FWD_BN;
+  static constexpr int RB = (D == 128) ? FAL_FWD_RB128 : 1;
 };
 
 template <int D>
 static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
-  constexpr int NW = FwdCfg<D>::NW, BN = FwdCfg<D>::BN;
+  constexpr int NW = FwdCfg<D>::NW, BN = FwdCfg<D>::BN, RB = FwdCfg<D>::RB;
   if (causal)
-    hipLaunchKernelGGL((fwd_kernel<D, NW, BN, true>), grid, dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((fwd_kernel<D, NW, BN, true, RB>), grid, dim3(NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((fwd_kernel<D, NW, BN, false>), grid, dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((fwd_kernel<D, NW, BN, false, RB>), grid, dim3(NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
 int fwd_block_m(int d) {
-  (void)d;
-  return 4 * 32;
+  switch (d) {
+    case 128: return FwdCfg<128>::NW * 32 * FwdCfg<128>::RB;
+    default: return 4 * 32;
+  }
 }
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st) {
