@@ -48,6 +48,10 @@ int check_operand(const char* name, const void* p, const int64_t* st, bool use_b
     if (st[i] % 8 != 0 || st[i] < 0)
       return fail(FAL_ERR_INVALID, "%s: stride[%d]=%lld must be a non-negative multiple of 8", name, i,
                   (long long)st[i]);
+  // kernels address a tile of up to 256 rows with 32-bit byte offsets
+  if (st[2] >= (int64_t(1) << 22))
+    return fail(FAL_ERR_UNSUPPORTED, "%s: sequence stride %lld elements is too large (limit 4194304)", name,
+                (long long)st[2]);
   return FAL_OK;
 }
 

@@ -125,22 +125,19 @@ fwd_kernel(FwdParams p) {
   const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
 
   // ---- per-lane addressing of the swizzled tiles ----
-  // Load instruction i of wave ws fills LDS chunks [(i*NW + ws)*64, +64): rows
-  // row0(I) .. of the tile, I = i*NW + ws.  Each instruction gets its own buffer
-  // resource starting at its first row, so rows past the end of the sequence fall
-  // outside the resource and are written as zeros; per-lane offsets are then
-  // independent of the tile (and, for head_dim 32/64/128, of i as well).
+  // Load instruction i of wave ws fills LDS chunks [(i*NW + ws)*64, +64) of the tile;
+  // the per-lane global offsets are relative to the tile's first row, so they do not
+  // depend on the tile.
   const int ws = __builtin_amdgcn_readfirstlane(w);   // wave index as a scalar
-  int kvo[IPT], vvo[IPT];
+  int kvo[IPT], vvo[IPT];             // byte offsets from the tile's first row
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
     const int I = i * NW + ws;
-    const int row0 = I * 64 / CPR;
     const int pch = I * 64 + lane;
     const int r = pch / CPR;
     const int cc = TL::logical_chunk(r, pch % CPR);
-    kvo[i] = (int)((r - row0) * p.k_ss + cc * 8) * 2;
-    vvo[i] = (int)((r - row0) * p.v_ss + cc * 8) * 2;
+    kvo[i] = (int)(r * p.k_ss + cc * 8) * 2;
+    vvo[i] = (int)(r * p.v_ss + cc * 8) * 2;
   }
   int kaddr[KS];                     // K fragment (row l32, chunk 2t+hh) for 32-key block 0
 #pragma unroll
@@ -156,20 +153,23 @@ fwd_kernel(FwdParams p) {
       for (int db = 0; db < DB; ++db) vaddr[hf][db] = TL::offset(hf * 8 + rl, db * 4 + cl) + 4 * (lane & 1);
   }
 
-  // Tile `tile` of K and V into LDS buffer `buf` without passing through VGPRs.
+  // Tile `tile` of K and V into LDS buffer `buf` without passing through VGPRs.  One
+  // buffer resource per tile starts at its first row and ends at the last key, so rows
+  // past the end of the sequence read as zeros.
   auto load_tile = [&](int tile, int buf) {
     const int n0 = tile * BN;
     half_t* kdst = smem + buf * 2 * PART;
     half_t* vdst = kdst + PART;
+    const int64_t left = (int64_t)max(nk - n0, 0);
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc(kbase + (int64_t)n0 * p.k_ss, (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff));
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc(vbase + (int64_t)n0 * p.v_ss, (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
       const int I = i * NW + ws;
-      const int r0 = n0 + I * 64 / CPR;           // first sequence row of this instruction
-      const int64_t left = (int64_t)max(nk - r0, 0);
-      const uint32_t kb = (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff);
-      const uint32_t vb = (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff);
-      buffer_to_lds16(make_rsrc(kbase + (int64_t)r0 * p.k_ss, kb), kvo[i], kdst + I * 64 * 8);
-      buffer_to_lds16(make_rsrc(vbase + (int64_t)r0 * p.v_ss, vb), vvo[i], vdst + I * 64 * 8);
+      buffer_to_lds16(krs, kvo[i], kdst + I * 64 * 8);
+      buffer_to_lds16(vrs, vvo[i], vdst + I * 64 * 8);
     }
   };
 
