@@ -439,13 +439,13 @@ bwd2_kernel(BwdParams p) {
   const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
   const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
 
-  // per-lane direct-load offsets (instruction i of wave ws fills chunks [(i*NW+ws)*64, +64))
-  // (in-tile offsets are 32-bit: buffer offsets are, and a tile spans < 2^31 bytes)
+  // per-lane direct-load byte offsets from a tile's first row (instruction i of wave ws
+  // fills chunks [(i*NW+ws)*64, +64)); one buffer resource per tile bounds the rows
   auto dl_offset = [&](int i, int64_t ss) {
     const int I = i * NW + ws;
     const int pch = I * 64 + lane;
     const int r = pch / CPR;
-    return ((r - I * 64 / CPR) * (int)ss + TL::logical_chunk(r, pch % CPR) * 8) * 2;
+    return (r * (int)ss + TL::logical_chunk(r, pch % CPR) * 8) * 2;
   };
   // Fragment reads (row l32 of a 32-row block, chunk 2t+hh) and transposed reads
   // (rows hf*8 + hh*4 + i/4 of a 16-row step, 32-column block db) of the swizzled
@@ -481,14 +481,18 @@ bwd2_kernel(BwdParams p) {
     const int key = kw0 + l32;
 
     __syncthreads();   // previous tile's readers of the LDS tiles are done
+    {
+      const int64_t left = (int64_t)max(nk - n0, 0);
+      const __amdgpu_buffer_rsrc_t krs =
+          make_rsrc(kbase + (int64_t)n0 * p.k_ss, (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff));
+      const __amdgpu_buffer_rsrc_t vrs =
+          make_rsrc(vbase + (int64_t)n0 * p.v_ss, (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
-    for (int i = 0; i < KIPT; ++i) {
-      const int I = i * NW + ws;
-      const int r0 = n0 + I * 64 / CPR;
-      const uint32_t kb = (uint32_t)min((int64_t)max(nk - r0, 0) * p.k_ss * 2, (int64_t)0x7fffffff);
-      buffer_to_lds16(make_rsrc(kbase + (int64_t)r0 * p.k_ss, kb), dl_offset(i, p.k_ss), ks_s + I * 64 * 8);
-      const uint32_t vb = (uint32_t)min((int64_t)max(nk - r0, 0) * p.v_ss * 2, (int64_t)0x7fffffff);
-      buffer_to_lds16(make_rsrc(vbase + (int64_t)r0 * p.v_ss, vb), dl_offset(i, p.v_ss), vs_s + I * 64 * 8);
+      for (int i = 0; i < KIPT; ++i) {
+        const int I = i * NW + ws;
+        buffer_to_lds16(krs, dl_offset(i, p.k_ss), ks_s + I * 64 * 8);
+        buffer_to_lds16(vrs, dl_offset(i, p.v_ss), vs_s + I * 64 * 8);
+      }
     }
 
     f32x16 dk_acc[DWB], dv_acc[DWB];
@@ -511,15 +515,14 @@ bwd2_kernel(BwdParams p) {
       const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)(q_off + q0) * p.q_ss;
       const half_t* dobase =
           p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)(q_off + q0) * p.do_ss;
+      const int64_t left = (int64_t)max(nq - q0, 0);
+      const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qbase, (uint32_t)min(left * p.q_ss * 2, (int64_t)0x7fffffff));
+      const __amdgpu_buffer_rsrc_t dors = make_rsrc(dobase, (uint32_t)min(left * p.do_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
       for (int i = 0; i < QIPT; ++i) {
         const int I = i * NW + ws;
-        const int r0 = I * 64 / CPR;
-        const int64_t left = (int64_t)max(nq - q0 - r0, 0);
-        buffer_to_lds16(make_rsrc(qbase + (int64_t)r0 * p.q_ss, (uint32_t)min(left * p.q_ss * 2, (int64_t)0x7fffffff)),
-                        dl_offset(i, p.q_ss), qd_s + (buf * 2 + 0) * QPART + I * 64 * 8);
-        buffer_to_lds16(make_rsrc(dobase + (int64_t)r0 * p.do_ss, (uint32_t)min(left * p.do_ss * 2, (int64_t)0x7fffffff)),
-                        dl_offset(i, p.do_ss), qd_s + (buf * 2 + 1) * QPART + I * 64 * 8);
+        buffer_to_lds16(qrs, dl_offset(i, p.q_ss), qd_s + (buf * 2 + 0) * QPART + I * 64 * 8);
+        buffer_to_lds16(dors, dl_offset(i, p.do_ss), qd_s + (buf * 2 + 1) * QPART + I * 64 * 8);
       }
       if (tid < BMQ) {
         float lv = INFINITY, dv = 0.f;
@@ -738,12 +741,11 @@ bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int i = 0; i < IPT; ++i) {
     const int I = i * NW + ws;
-    const int row0 = I * 64 / CPR;
     const int pch = I * 64 + lane;
     const int r = pch / CPR;
     const int cc = TL::logical_chunk(r, pch % CPR);
-    kvo[i] = (int)((r - row0) * p.k_ss + cc * 8) * 2;
-    vvo[i] = (int)((r - row0) * p.v_ss + cc * 8) * 2;
+    kvo[i] = (int)(r * p.k_ss + cc * 8) * 2;   // from the tile's first row
+    vvo[i] = (int)(r * p.v_ss + cc * 8) * 2;
   }
   int kaddr[KS];   // fragment (row l32, chunk 2t+hh) of 32-key block 0
 #pragma unroll
@@ -763,15 +765,16 @@ bwd_dq_kernel(BwdParams p) {
     const int n0 = tile * BN;
     half_t* kdst = smem + buf * 2 * PART;
     half_t* vdst = kdst + PART;
+    const int64_t left = (int64_t)max(nk - n0, 0);
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc(kbase + (int64_t)n0 * p.k_ss, (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff));
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc(vbase + (int64_t)n0 * p.v_ss, (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
       const int I = i * NW + ws;
-      const int r0 = n0 + I * 64 / CPR;
-      const int64_t left = (int64_t)max(nk - r0, 0);
-      const uint32_t kb = (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff);
-      const uint32_t vb = (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff);
-      buffer_to_lds16(make_rsrc(kbase + (int64_t)r0 * p.k_ss, kb), kvo[i], kdst + I * 64 * 8);
-      buffer_to_lds16(make_rsrc(vbase + (int64_t)r0 * p.v_ss, vb), vvo[i], vdst + I * 64 * 8);
+      buffer_to_lds16(krs, kvo[i], kdst + I * 64 * 8);
+      buffer_to_lds16(vrs, vvo[i], vdst + I * 64 * 8);
     }
   };
 
