@@ -595,14 +595,17 @@ bwd2_kernel(BwdParams p) {
 
     // ---- sum the two query halves' dK/dV and write this tile's rows ----
     __syncthreads();
-    float* red = reinterpret_cast<float*>(qd_s);   // [kg][32 keys][D] fp32
+    // The partner waves (same key group, same lane layout) meet in LDS: the second
+    // query half stages its accumulators lane-contiguous, [kg][db][i][lane], and the
+    // first adds them element by element (bank-conflict free, no transpose).
+    float* red = reinterpret_cast<float*>(qd_s);
     auto reduce_write = [&](f32x16 (&acc)[DWB], half_t* row, float sc) {
+      float* mine = red + (size_t)kg * DWB * 16 * 64 + lane;
       if (qh == 1) {
 #pragma unroll
         for (int db = 0; db < DWB; ++db)
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            red[(kg * 32 + l32) * D + db * 32 + (i >> 2) * 8 + hh * 4 + (i & 3)] = acc[db][i];
+          for (int i = 0; i < 16; ++i) mine[(db * 16 + i) * 64] = acc[db][i];
       }
       __syncthreads();
       if (qh == 0 && key < nk) {
@@ -611,10 +614,9 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             const int col = db * 32 + g4 * 8 + hh * 4;
-            const f32x4 o = *reinterpret_cast<const f32x4*>(&red[(kg * 32 + l32) * D + col]);
             half4 h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)((acc[db][g4 * 4 + e] + o[e]) * sc);
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)((acc[db][g4 * 4 + e] + mine[(db * 16 + g4 * 4 + e) * 64]) * sc);
             *reinterpret_cast<half4*>(row + col) = h;
           }
       }
