@@ -375,11 +375,16 @@ bwd_kernel(BwdParams p) {
 // n-1-kt, so all workgroups do the same amount of work.  The two query halves'
 // dK/dV partials are summed in LDS.
 // --------------------------------------------------------------------------
+#ifndef FAL_BWD2_NW
+#define FAL_BWD2_NW 4   // waves per workgroup: 4 (64 keys, 2 workgroups per CU) or 8 (128 keys, double-buffered Q/dO)
+#endif
 template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(512)
+__global__ void __launch_bounds__(FAL_BWD2_NW * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
 bwd2_kernel(BwdParams p) {
   using TL = SwizzledTile<D>;
-  constexpr int NW = 8, BN = 128, BMQ = 64;
+  constexpr int NW = FAL_BWD2_NW, BN = NW * 16, BMQ = 64;
+  constexpr int NKG = NW / 2;             // key groups of 32 (x 2 query halves)
+  constexpr bool DBUF = NW == 8;          // Q/dO double buffer (else one buffer, 2 WG/CU)
   constexpr int KS = D / 16;
   constexpr int DWB = D / 32;
   constexpr int CPR = TL::CPR;
@@ -388,11 +393,11 @@ bwd2_kernel(BwdParams p) {
   constexpr int KIPT = BN * CPR / (NW * 64);
   constexpr int QIPT = BMQ * CPR / (NW * 64);
   static_assert(BMQ * CPR % (NW * 64) == 0, "Q tile must split evenly over the waves");
-  static_assert(2 * 2 * QPART * 2 >= 4 * 32 * D * 4, "dK/dV reduction reuses the Q/dO buffers");
+  static_assert((DBUF ? 2 : 1) * 2 * QPART * 2 >= NKG * 32 * D * 4, "dK/dV reduction reuses the Q/dO buffers");
 
   __shared__ __attribute__((aligned(1024))) half_t ks_s[KPART];
   __shared__ __attribute__((aligned(1024))) half_t vs_s[KPART];
-  __shared__ __attribute__((aligned(1024))) half_t qd_s[2 * 2 * QPART];   // [buffer][Q, dO]
+  __shared__ __attribute__((aligned(1024))) half_t qd_s[(DBUF ? 2 : 1) * 2 * QPART];   // [buffer][Q, dO]
   __shared__ float l_s[2][BMQ];
   __shared__ float d_s[2][BMQ];
 
@@ -400,8 +405,8 @@ bwd2_kernel(BwdParams p) {
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int ws = __builtin_amdgcn_readfirstlane(w);
-  const int kg = w & 3;                   // key group
-  const int qh = w >> 2;                  // query half
+  const int kg = w % NKG;                 // key group
+  const int qh = w / NKG;                 // query half
   const int l32 = lane & 31;
   const int hh = lane >> 5;
 
@@ -540,7 +545,7 @@ bwd2_kernel(BwdParams p) {
     if (nitems_q > 0) fetch(0, 0);
     for (int item = 0; item < nitems_q; ++item) {
       {
-        const int buf = item & 1;
+        const int buf = DBUF ? (item & 1) : 0;
         const int q0 = (qt0 + item % ntq) * BMQ;
         wait_vmcnt0();
         if (tid < BMQ) {
@@ -548,7 +553,7 @@ bwd2_kernel(BwdParams p) {
           d_s[buf][tid] = dpre;
         }
         __syncthreads();                  // barrier A: item in LDS; readers of item-1 done
-        if (item + 1 < nitems_q) fetch(item + 1, buf ^ 1);
+        if (DBUF && item + 1 < nitems_q) fetch(item + 1, buf ^ 1);
         const half_t* q_s = qd_s + (buf * 2 + 0) * QPART + qh * 32 * CPR * 8;
         const half_t* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
         const int qr0 = q0 + qh * 32;     // first query row of this wave's half
@@ -589,6 +594,10 @@ bwd2_kernel(BwdParams p) {
               FAL_BWD_FENCE();
             }
           }
+        }
+        if (!DBUF && item + 1 < nitems_q) {
+          __syncthreads();                // barrier B: every wave is done with this item's tile
+          fetch(item + 1, 0);
         }
       }
     }
@@ -889,8 +898,7 @@ bwd_dq_kernel(BwdParams p) {
 constexpr int kBwdNW = 4;
 
 int bwd_block_n(int d) {
-  (void)d;
-  return kBwdNW * 32;
+  return (d == 64 || d == 128) ? FAL_BWD2_NW * 16 : kBwdNW * 32;
 }
 
 template <int D>
@@ -899,9 +907,9 @@ static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStr
     // batched causal: one workgroup per pair of key tiles
     if (!p.cu_q && causal) grid.x = (unsigned)((p.n_ktiles + 1) / 2) * p.B * p.Hkv;
     if (causal)
-      hipLaunchKernelGGL((bwd2_kernel<D, true>), grid, dim3(512), 0, st, p);
+      hipLaunchKernelGGL((bwd2_kernel<D, true>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
     else
-      hipLaunchKernelGGL((bwd2_kernel<D, false>), grid, dim3(512), 0, st, p);
+      hipLaunchKernelGGL((bwd2_kernel<D, false>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
   } else {
     if (causal)
       hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, true>), grid, dim3(kBwdNW * 64), 0, st, p);
