@@ -254,7 +254,8 @@ decode_split_kernel(DecodeParams p) {
   }
 }
 
-// One wave per (sequence, query head): merge the splits' partial outputs.
+// One wave per (sequence, query head): merge the splits' partial outputs, sixteen splits
+// per round trip.
 template <int D>
 __global__ void __launch_bounds__(64)
 decode_combine_kernel(DecodeParams p) {
@@ -262,50 +263,48 @@ decode_combine_kernel(DecodeParams p) {
   const int b = blockIdx.y;
   const int lane = threadIdx.x;
   const int L = p.seqlens[b];
-  const int ns = cdiv(L, p.chunk);
+  const int ns = cdiv(max(L, 0), p.chunk);
   const int64_t base = ((int64_t)b * p.Hq + hq) * p.max_splits;
-  float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, p.part_m[base + s]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-  const float M_use = (M == -INFINITY) ? 0.f : M;
   constexpr int DJ = (D + 63) / 64;
+  constexpr int CH = 16;   // splits whose loads are all in flight together
   float acc[DJ];
 #pragma unroll
   for (int j = 0; j < DJ; ++j) acc[j] = 0.f;
-  float wsum = 0.f;
-  auto add_split = [&](float pm, const float* po) {
-    const float wgt = fast_exp2(pm - M_use);
-    wsum += wgt;
+  float M = -INFINITY, wsum = 0.f;
+  // chunks of CH splits, merged with an online max: every load of a chunk is issued
+  // before any of them is used
+  for (int s0 = 0; s0 < ns; s0 += CH) {
+    float pm[CH], x[CH][DJ];
 #pragma unroll
-    for (int j = 0; j < DJ; ++j) {
-      const int d = lane + 64 * j;
-      if (d < D) acc[j] = fmaf(wgt, po[d], acc[j]);
+    for (int u = 0; u < CH; ++u) {
+      const bool ok = s0 + u < ns;
+      pm[u] = ok ? p.part_m[base + s0 + u] : -INFINITY;
+      const float* po = p.part_o + (base + s0 + u) * D;
+#pragma unroll
+      for (int j = 0; j < DJ; ++j) x[u][j] = (ok && lane + 64 * j < D) ? po[lane + 64 * j] : 0.f;
     }
-  };
-  int s = 0;
-  for (; s + 8 <= ns; s += 8) {   // eight splits' loads in flight per lane
-    float pm[8], x[8][DJ];
+    float cm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      pm[u] = p.part_m[base + s + u];
-      const float* po = p.part_o + (base + s + u) * D;
+    for (int u = 0; u < CH; ++u) cm = fmaxf(cm, pm[u]);
+    const float Mn = fmaxf(M, cm);
+    if (Mn == -INFINITY) continue;
+    const float r = fast_exp2(M - Mn);   // 0 on the first chunk with a finite max
+    wsum *= r;
 #pragma unroll
-      for (int j = 0; j < DJ; ++j) x[u][j] = (lane + 64 * j < D) ? po[lane + 64 * j] : 0.f;
-    }
+    for (int j = 0; j < DJ; ++j) acc[j] *= r;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float wgt = fast_exp2(pm[u] - M_use);
+    for (int u = 0; u < CH; ++u) {
+      const float wgt = fast_exp2(pm[u] - Mn);
       wsum += wgt;
 #pragma unroll
       for (int j = 0; j < DJ; ++j) acc[j] = fmaf(wgt, x[u][j], acc[j]);
     }
+    M = Mn;
   }
-  for (; s < ns; ++s) add_split(p.part_m[base + s], p.part_o + (base + s) * D);
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   half_t* orow = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
 #pragma unroll
-  for (int j = 0; j < (D + 63) / 64; ++j) {
+  for (int j = 0; j < DJ; ++j) {
     const int d = lane + 64 * j;
     if (d < D) orow[d] = (half_t)(acc[j] * inv);
   }
