@@ -245,16 +245,22 @@ static int fill_bwd_common(BwdParams& p, const void* dout, const void* q, const 
 }
 
 static int run_bwd(BwdParams& p, int d, int causal, dim3 grid, dim3 dq_grid, bool batched, hipStream_t st) {
-  hipError_t e = launch_bwd_pre(p, d, batched ? 1 : 0, st);
+  hipError_t e;
+  if (bwd_split_dq(d)) {
+    // dQ kernel first: it also computes D = rowsum(dO * O), which the dK/dV kernel
+    // reads, so no preprocessing launch is needed
+    if (dq_grid.x > 0 && dq_grid.y > 0) {
+      e = launch_bwd_dq(p, d, causal, dq_grid, st);
+      if (e != hipSuccess) return launch_status(e, "bwd dq");
+    }
+    if (grid.x > 0 && grid.y > 0) return launch_status(launch_bwd(p, d, causal, grid, st), "bwd main");
+    return ok();
+  }
+  e = launch_bwd_pre(p, d, batched ? 1 : 0, st);
   if (e != hipSuccess) return launch_status(e, "bwd preprocess");
   if (grid.x > 0 && grid.y > 0) {
     e = launch_bwd(p, d, causal, grid, st);
     if (e != hipSuccess) return launch_status(e, "bwd main");
-  }
-  if (bwd_split_dq(d)) {
-    if (dq_grid.x == 0 || dq_grid.y == 0) return ok();
-    e = launch_bwd_dq(p, d, causal, dq_grid, st);
-    return launch_status(e, "bwd dq");
   }
   e = launch_bwd_post(p, d, st);
   return launch_status(e, "bwd dq cast");

@@ -723,24 +723,33 @@ bwd_dq_kernel(BwdParams p) {
   const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
   const int64_t lrow = (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
 
-  // Q and dO slices of this wave (B operands: n = query row, k = head dim), and the
-  // row's log-sum-exp (log2 domain) and delta
+  // Q and dO slices of this wave (B operands: n = query row, k = head dim), the row's
+  // log-sum-exp (log2 domain) and D = rowsum(dO * O).  The two lanes of a row hold one
+  // half of the head dim each.  D is also stored for the dK/dV kernel, which runs after
+  // this one.
   const int row = m0 + w * 32 + l32;
   half8 qreg[KS], doreg[KS];
-  float lrow2 = INFINITY, drow = 0.f;
+  float lrow2 = INFINITY, dpart = 0.f;
   if (row < nq) {
+    const half_t* orow = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)(q_off + row) * p.o_ss;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       qreg[t] = load_h8(qbase + (int64_t)row * p.q_ss + t * 16 + hh * 8);
       doreg[t] = load_h8(dobase + (int64_t)row * p.do_ss + t * 16 + hh * 8);
+      const half8 ov = load_h8(orow + t * 16 + hh * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dpart = __builtin_amdgcn_fdot2(half2v{doreg[t][2 * j], doreg[t][2 * j + 1]}, half2v{ov[2 * j], ov[2 * j + 1]},
+                                       dpart, false);
     }
     const float L = p.lse[lrow + (int64_t)row * p.l_ss];
     lrow2 = (L == -INFINITY) ? INFINITY : L * kLog2e;
-    drow = p.delta[lrow + (int64_t)row * p.l_ss];
   } else {
 #pragma unroll
     for (int t = 0; t < KS; ++t) qreg[t] = doreg[t] = zero_h8();
   }
+  const float drow = pair_sum(dpart);
+  if (hh == 0 && row < nq) p.delta[lrow + (int64_t)row * p.l_ss] = drow;
   const float c = p.scale_log2;
 
   const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
