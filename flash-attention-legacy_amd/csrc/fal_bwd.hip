@@ -514,9 +514,16 @@ bwd2_kernel(BwdParams p) {
     const int ntq = nqt > qt0 ? nqt - qt0 : 0;
     const int nitems_q = G * ntq;
     float lpre = 0.f, dpre = 0.f;
-    auto fetch = [&](int item, int buf) {
-      const int hq = hkv * G + item / ntq;
-      const int q0 = (qt0 + item % ntq) * BMQ;
+    // the next item to fetch, (query head, query tile), walked with counters: the
+    // scalar unit has no divide
+    int f_hq = hkv * G, f_qt = qt0;
+    auto fetch = [&](int buf) {
+      const int hq = f_hq;
+      const int q0 = f_qt * BMQ;
+      if (++f_qt == nqt) {
+        f_qt = qt0;
+        ++f_hq;
+      }
       const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)(q_off + q0) * p.q_ss;
       const half_t* dobase =
           p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)(q_off + q0) * p.do_ss;
@@ -542,18 +549,20 @@ bwd2_kernel(BwdParams p) {
       }
     };
 
-    if (nitems_q > 0) fetch(0, 0);
+    if (nitems_q > 0) fetch(0);
+    int c_qt = qt0;   // query tile of the current item
     for (int item = 0; item < nitems_q; ++item) {
       {
         const int buf = DBUF ? (item & 1) : 0;
-        const int q0 = (qt0 + item % ntq) * BMQ;
+        const int q0 = c_qt * BMQ;
+        if (++c_qt == nqt) c_qt = qt0;
         wait_vmcnt0();
         if (tid < BMQ) {
           l_s[buf][tid] = lpre;
           d_s[buf][tid] = dpre;
         }
         __syncthreads();                  // barrier A: item in LDS; readers of item-1 done
-        if (DBUF && item + 1 < nitems_q) fetch(item + 1, buf ^ 1);
+        if (DBUF && item + 1 < nitems_q) fetch(buf ^ 1);
         const half_t* q_s = qd_s + (buf * 2 + 0) * QPART + qh * 32 * CPR * 8;
         const half_t* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
         const int qr0 = q0 + qh * 32;     // first query row of this wave's half
@@ -597,7 +606,7 @@ bwd2_kernel(BwdParams p) {
         }
         if (!DBUF && item + 1 < nitems_q) {
           __syncthreads();                // barrier B: every wave is done with this item's tile
-          fetch(item + 1, 0);
+          fetch(0);
         }
       }
     }
