@@ -576,7 +576,11 @@ bwd2_kernel(BwdParams p) {
             dp = mfma32(load_h8(do_s + fa), load_h8(vs_s + fa + kg * 32 * CPR * 8), dp);
             FAL_BWD_FENCE();
           }
-          // P and dS; element i: query qr0 + (i/4)*8 + hh*4 + i%4, key `key`
+          // P and dS; element i: query qr0 + (i/4)*8 + hh*4 + i%4, key `key`.
+          // Query rows past the end carry L = +inf (P = 0), and keys past the end only
+          // feed dK/dV rows that are never written, so the causal test is the only mask:
+          // key > query  <=>  key - qr0 - hh*4 > (i/4)*8 + i%4, a constant per element.
+          const int cthr = key - qr0 - hh * 4;
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             const f32x4 lv = *reinterpret_cast<const f32x4*>(&l_s[buf][qh * 32 + g4 * 8 + hh * 4]);
@@ -584,9 +588,8 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int i = g4 * 4 + e;
-              const int qrow = qr0 + g4 * 8 + hh * 4 + e;
               float pv = fast_exp2(fmaf(s[i], c, -lv[e]));
-              if (key >= nk || qrow >= nq || (CAUSAL && key > qrow)) pv = 0.f;
+              if (CAUSAL && cthr > g4 * 8 + e) pv = 0.f;
               s[i] = pv;
               dp[i] = pv * (dp[i] - dv[e]);
             }
