@@ -194,7 +194,11 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
   p.cu_q = cu_seqlens_q;
   p.cu_k = cu_seqlens_k;
   p.work = work;
-  return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_q), st),
+  p.n_qtiles = cap;   // work-list capacity
+  const int64_t groups8 = ((int64_t)cap * heads_kv + 7) / 8 * 8;
+  const int64_t nblocks = groups8 * (heads_q / heads_kv);
+  if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
+  return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), st),
                        "fal_fwd_varlen");
 }
 

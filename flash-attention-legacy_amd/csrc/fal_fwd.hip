@@ -60,9 +60,19 @@ fwd_kernel(FwdParams p) {
   // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
   int b, hq, qt, q_off, k_off, nq, nk;
   if (p.cu_q) {
-    const int2 wk = p.work[blockIdx.x];
+    // 1-D grid over (work item, KV head) groups of G query heads.  Block i runs on XCD
+    // i % 8 as that XCD's (i / 8)-th block; the groups are dealt to the XCDs round-robin
+    // in work-list order (heaviest first), and the G heads of a group, which read the
+    // same K/V, run back to back on one XCD (one L2).  The grid is padded to a multiple
+    // of 8 groups; padding blocks exit.
+    const int g = p.Hq / p.Hkv;
+    const int k8 = blockIdx.x >> 3;
+    const int grp = (k8 / g) * 8 + (blockIdx.x & 7);
+    const int item = grp / p.Hkv;
+    if (item >= p.n_qtiles) return;
+    const int2 wk = p.work[item];
     if (wk.x < 0) return;
-    hq = blockIdx.y;
+    hq = (grp % p.Hkv) * g + k8 % g;
     b = 0;
     qt = wk.y;
     q_off = p.cu_q[wk.x];
