@@ -420,9 +420,12 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int tile, int n
 #ifndef FAL_FWD_RB128
 #define FAL_FWD_RB128 1   // 32-row blocks per wave for head_dim 128
 #endif
+#ifndef FAL_FWD_NW128
+#define FAL_FWD_NW128 4   // waves per workgroup for head_dim 128
+#endif
 template <int D>
 struct FwdCfg {
-  static constexpr int NW = 4;
+  static constexpr int NW = D == 128 ? FAL_FWD_NW128 : 4;
   static constexpr int BN = (D >= 256) ? 32 : FAL_FWD_BN;
   static constexpr int RB = (D == 128) ? FAL_FWD_RB128 : 1;
 };
