@@ -13,7 +13,8 @@
 //   operand, V rows go through a wave-private LDS slab and come back transposed
 //   (ds_read_b64_tr_b16) as the A operand of O^T = V^T P^T.  The next slice's loads
 //   are issued before the current slice is consumed.
-// * The waves' (max, sum, O) are merged in LDS and the workgroup writes one
+// * The waves' (max, sum, O) are merged in LDS, in a fixed order (the output is
+//   deterministic), and the workgroup writes one
 //   normalised partial O (fp32) and its log2-domain LSE.
 // Combine kernel: one wave per (sequence, query head) merges its splits.
 #include <type_traits>
@@ -72,7 +73,6 @@ decode_split_kernel(DecodeParams p) {
   __shared__ float m_s[NW][16];
   __shared__ float l_s[NW][16];
   __shared__ float inv_s[16];
-  __shared__ float o_s[16 * D];
 
   const int nhg = cdiv(p.Hq / p.Hkv, 16);
   const int heads_tiles = p.Hkv * nhg;
@@ -98,7 +98,6 @@ decode_split_kernel(DecodeParams p) {
   const int hbase = hkv * G + hg * 16;           // first query head of this tile
   const int nh = min(16, G - hg * 16);
 
-  for (int i = tid; i < 16 * D; i += NW * 64) o_s[i] = 0.f;
 
   const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
   const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
@@ -233,11 +232,15 @@ decode_split_kernel(DecodeParams p) {
   for (int i = 0; i < NW; ++i) M = fmaxf(M, m_s[i][l16]);
   const float M_use = (M == -INFINITY) ? 0.f : M;
   const float wscale = fast_exp2(m_run - M_use);
+  // Each wave's rescaled O goes to its own (now idle) V ring slab; the slabs are summed
+  // in wave order below, so the result does not depend on timing.
+  float* part = reinterpret_cast<float*>(&vsm[ws][0]);
+  static_assert(sizeof(vsm[0]) >= 16 * D * sizeof(float), "a wave's slab holds its partial O");
   if (l16 < nh) {
 #pragma unroll
     for (int db = 0; db < DBN; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(&o_s[l16 * D + db * 16 + 4 * g4 + i], oacc[db][i] * wscale);
+      for (int i = 0; i < 4; ++i) part[l16 * D + db * 16 + 4 * g4 + i] = oacc[db][i] * wscale;
   }
   const int64_t pbase = ((int64_t)b * p.Hq + hbase) * p.max_splits + split;
   if (w == 0 && lane < nh) {
@@ -250,7 +253,10 @@ decode_split_kernel(DecodeParams p) {
   __syncthreads();
   for (int i = tid; i < nh * D; i += NW * 64) {
     const int h = i / D, d = i % D;
-    p.part_o[(pbase + (int64_t)h * p.max_splits) * D + d] = o_s[h * D + d] * inv_s[h];
+    float o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) o += reinterpret_cast<const float*>(&vsm[ww][0])[h * D + d];
+    p.part_o[(pbase + (int64_t)h * p.max_splits) * D + d] = o * inv_s[h];
   }
 }
 

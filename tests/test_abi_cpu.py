@@ -120,3 +120,15 @@ def test_device_supported_without_gpu(ext):
     if torch.cuda.is_available():
         pytest.skip("GPU host")
     assert ext.device_supported(0) is False
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """No CPU fallback: without the HIP library the package does not import."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "try:\n    import flash_attn_legacy\nexcept ImportError as e:\n"
+            "    print('IMPORTERROR', e)\nelse:\n    print('IMPORTED')\n") % os.path.join(ROOT, "flash-attention-legacy_amd")
+    env = dict(os.environ, FLASH_ATTN_LEGACY_LIB=str(tmp_path / "missing.so"))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert "IMPORTERROR" in r.stdout and "HIP library not found" in r.stdout, r.stdout + r.stderr

@@ -1,0 +1,68 @@
+"""The kernels' launch sequences contain no memset or host synchronisation, so a
+caller can capture them in a HIP graph.  Each entry point is captured once and the
+graph is replayed several times, with eager work and synchronisations between the
+replays; every replay must reproduce the eager result bit for bit."""
+
+import math
+
+import pytest
+import torch
+
+from helpers import randn
+
+pytestmark = pytest.mark.gpu
+
+
+def replay_check(fn, eager_out, n=4):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()   # warm-up on the capture stream (allocator pools)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = fn()
+    for r in range(n):
+        # unrelated eager work between replays
+        junk = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        for t in outs:
+            t.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for idx, (got, ref) in enumerate(zip(outs, eager_out)):
+            same = torch.equal(got, ref) or (torch.equal(torch.isnan(got), torch.isnan(ref)) and
+                                             torch.equal(torch.nan_to_num(got), torch.nan_to_num(ref)))
+            assert same, (f"replay {r}, output {idx}: nan {int(torch.isnan(got).sum())} vs "
+                          f"{int(torch.isnan(ref).sum())}, max diff "
+                          f"{float((torch.nan_to_num(got).float() - torch.nan_to_num(ref).float()).abs().max())}")
+        del junk
+
+
+def test_graph_forward_backward():
+    from flash_attn_legacy import hip_ext
+    B, Hq, Hkv, N, d = 2, 8, 2, 384, 128
+    q, k, v, do = randn((B, Hq, N, d), seed=1), randn((B, Hkv, N, d), seed=2), randn((B, Hkv, N, d), seed=3), \
+        randn((B, Hq, N, d), seed=4)
+    scale = 1.0 / math.sqrt(d)
+    o, lse = hip_ext.forward(q, k, v, scale, True)
+    grads = hip_ext.backward(do, q, k, v, o, lse, scale, True)
+    torch.cuda.synchronize()
+    replay_check(lambda: tuple(hip_ext.forward(q, k, v, scale, True)), (o, lse))
+    replay_check(lambda: tuple(hip_ext.backward(do, q, k, v, o, lse, scale, True)), tuple(grads))
+
+
+def test_graph_varlen_and_decode():
+    from flash_attn_legacy import hip_ext
+    lens = [5, 130, 257, 64]
+    cu = torch.tensor([0, 5, 135, 392, 456], dtype=torch.int32, device="cuda")
+    tot = sum(lens)
+    q, k, v = randn((tot, 8, 64), seed=5), randn((tot, 4, 64), seed=6), randn((tot, 4, 64), seed=7)
+    o, lse = hip_ext.forward_varlen(q, k, v, cu, cu, max(lens), max(lens), 0.125, True)
+    replay_check(lambda: tuple(hip_ext.forward_varlen(q, k, v, cu, cu, max(lens), max(lens), 0.125, True)), (o, lse))
+    seq = torch.tensor([1, 700, 3000, 129], dtype=torch.int32, device="cuda")
+    qd = randn((4, 16, 128), seed=8)
+    kc, vc = randn((4, 3000, 4, 128), seed=9), randn((4, 3000, 4, 128), seed=10)
+    od, ld = hip_ext.decode(qd, kc, vc, seq, 0.088, return_lse=True)
+    replay_check(lambda: tuple(hip_ext.decode(qd, kc, vc, seq, 0.088, return_lse=True)), (od, ld))
