@@ -6,19 +6,20 @@
 // dK += dS^T Q; dQ += dS K accumulated in fp32 and cast at the end; dK/dV of a KV
 // head sum over all query heads of its GQA group inside one workgroup.
 //
-// Work decomposition: one workgroup owns BN = 32*NW keys of one KV head and walks
-// every (query head of the group, query tile of BMQ rows) that can see them.
-// * Each wave owns 32 keys.  Its K and V rows live in VGPRs as the B operands of
-//   S = Q K^T and dP = dO V^T, so those accumulators hold one key per lane.
-// * P and dS leave the accumulators straight into the B operands of
-//   dV^T += dO^T P and dK^T += Q^T dS; dO^T and Q^T come from the row-major
-//   Q/dO tiles in LDS via ds_read_b64_tr_b16.  dK^T / dV^T stay in registers
-//   for the whole kernel.
-// * dS^T is staged in LDS (fp16) and each wave then computes one 32-column
-//   block of dQ = dS K for the tile (K^T from the LDS K tile, again via the
-//   transposed read) and adds it to the fp32 dQ accumulator with global atomics.
-// * For head_dim 256 the dK/dV accumulators are split into two passes over the
-//   query tiles (128 columns each); dQ is produced in the first pass.
+// Kernels:
+// * head_dim 64/128 (FA2's split form, no atomics, deterministic):
+//   - bwd_dq_kernel (query-outer, runs first): a workgroup owns 128 query rows;
+//     Q and dO stay in VGPRs, K/V tiles stream through LDS; it computes D for its
+//     rows, P, dS and dQ = dS K, written once in fp16;
+//   - bwd2_kernel (KV-outer): a workgroup owns 64 keys of one KV head and walks every
+//     (query head of the group, query tile) that can see them; P and dS leave the
+//     accumulators straight into the B operands of dV^T += dO^T P and
+//     dK^T += Q^T dS (dO^T and Q^T from the Q/dO tiles via ds_read_b64_tr_b16);
+//     dK/dV stay in registers until the end.
+// * head_dim 32/96/256: bwd_pre_kernel (D, zeroed fp32 dQ accumulator), bwd_kernel
+//   (KV-outer, dS^T staged in LDS, dQ = dS K added with fp32 atomics; for head_dim
+//   256 the dK/dV accumulators take two passes of 128 columns) and bwd_post_kernel
+//   (dQ cast to fp16).
 #include <type_traits>
 
 #include "fal_kernels.h"

@@ -6,13 +6,17 @@
 // O = sum(p v) / sum(p); L = max + ln(max(sum, 1e-20)) in natural log; a row with no
 // valid key gives O = 0 and L = -inf.
 //
-// Work decomposition (one workgroup = NW waves = 32*NW query rows of one head):
-// * each wave owns 32 query rows; its Q slice stays in VGPRs for the whole kernel as
-//   the B operand of S^T = K Q^T, so the accumulator puts one query row per lane
-//   (two lanes per row, one per wave half) and row max / row sum are in-lane plus
-//   one permlane32 swap;
-// * K/V tiles of BN keys are staged row-major in LDS, double-buffered, and fetched
-//   one tile ahead into registers with 16-byte global loads;
+// Work decomposition (one workgroup = NW waves = 32*NW*RB query rows of one head):
+// * each wave owns 32 query rows (RB = 1); its Q slice, pre-multiplied by
+//   scale*log2(e), stays in VGPRs for the whole kernel as the B operand of
+//   S^T = K Q^T, so the accumulator puts one query row per lane (two lanes per row,
+//   one per wave half) and row reductions are in-lane plus one permlane32 swap;
+// * K/V tiles of BN keys are copied HBM -> LDS by buffer loads that bypass VGPRs,
+//   into XOR-swizzled, double-buffered tiles (conflict-free row and transposed
+//   reads); one buffer resource per tile zero-fills rows past the sequence end;
+// * the S^T accumulators start at -m (the row's reference max), so the MFMAs give
+//   the exponent of P directly; the row max is recomputed only when a tile's P
+//   could leave fp16 range (its per-lane p sum exceeds 2^15) or on a row's first tile;
 // * P^T goes straight from the S^T accumulator into the B operand of O^T = V^T P^T;
 //   V^T comes from the row-major V tile through ds_read_b64_tr_b16;
 // * causal tiles above the diagonal are never visited; fully-masked waves inside a
