@@ -5,18 +5,21 @@
 // s = q k^T * scale (+ additive mask), softmax over the keys, @ v.  This file computes
 // the same result without materialising the repeated K/V or the score row.
 //
-// Split kernel: one workgroup per (split, kv head, sequence) covers `chunk` cache rows.
-// * All G = Hq/Hkv query heads of the KV head ride in one MFMA tile: S^T = K Q^T with
-//   M = 32 cache rows and N = the G heads (padded to 32 lanes), so every K/V byte is
-//   read once from HBM for the whole group.
-// * Each wave streams its own 32-row slices: K rows are loaded straight into the A
-//   operand, V rows go through a wave-private LDS slab and come back transposed
-//   (ds_read_b64_tr_b16) as the A operand of O^T = V^T P^T.  The next slice's loads
-//   are issued before the current slice is consumed.
-// * The waves' (max, sum, O) are merged in LDS, in a fixed order (the output is
-//   deterministic), and the workgroup writes one
-//   normalised partial O (fp32) and its log2-domain LSE.
-// Combine kernel: one wave per (sequence, query head) merges its splits.
+// Schedule kernel: turns cache_seqlens into a longest-first list of (sequence, split)
+// work items on the device (no host synchronisation).
+// Split kernel: one workgroup per (work item, KV head, group of up to 16 query heads)
+// covers `chunk` cache rows.
+// * The query heads of the KV head ride in one 16x16x32 MFMA tile: S^T = K Q^T with
+//   M = 16 cache rows and N = the heads, so every K/V byte is read once from HBM for
+//   the whole group.
+// * Each wave streams its own 32-row steps, two steps ahead: K rows are loaded
+//   straight into the A operand, V rows go through a wave-private LDS ring (buffer
+//   loads with the nontemporal bit) and come back transposed (ds_read_b64_tr_b16) as
+//   the A operand of O^T = V^T P^T.
+// * The waves' (max, sum, O) are merged in LDS in a fixed order (the output is
+//   deterministic); the workgroup writes one normalised partial O (fp32) and its
+//   log2-domain LSE.
+// Combine kernel: one wave per (sequence, query head) merges the splits' partials.
 #include <type_traits>
 
 #include "fal_kernels.h"
