@@ -384,7 +384,11 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
     e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, bm, nbq, is_causal ? 1 : 0, qwork, capq, st);
     if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen dq schedule");
     p.qwork = qwork;
-    dq_grid = dim3((unsigned)capq, (unsigned)heads_q);
+    p.n_qitems = capq;
+    const int64_t groups8 = ((int64_t)capq * heads_kv + 7) / 8 * 8;
+    const int64_t nblocks = groups8 * (heads_q / heads_kv);
+    if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
+    dq_grid = dim3((unsigned)nblocks);
   }
   return run_bwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_kv), dq_grid, false, st);
 }

@@ -691,9 +691,17 @@ bwd_dq_kernel(BwdParams p) {
 
   int b, hq, qt_a, qt_b = -1, q_off, k_off, nq, nk;
   if (p.cu_q) {
-    const int2 wk = p.qwork[blockIdx.x];
+    // 1-D grid: (work item, KV head) groups dealt round-robin to the 8 XCDs in list
+    // order, the query heads of a group back to back on one XCD (they read the same
+    // K/V); the grid is padded to a multiple of 8 groups
+    const int g = p.Hq / p.Hkv;
+    const int k8 = blockIdx.x >> 3;
+    const int grp = (k8 / g) * 8 + (blockIdx.x & 7);
+    const int item = grp / p.Hkv;
+    if (item >= p.n_qitems) return;
+    const int2 wk = p.qwork[item];
     if (wk.x < 0) return;
-    hq = blockIdx.y;
+    hq = (grp % p.Hkv) * g + k8 % g;
     b = 0;
     qt_a = wk.y;
     q_off = p.cu_q[wk.x];

@@ -64,6 +64,7 @@ struct BwdParams {
   const int* cu_k;
   const int2* work;   // (sequence, kv-tile) list in varlen mode
   const int2* qwork;  // (sequence, query-tile) list of the dQ kernel in varlen mode
+  int n_qitems;       // capacity of qwork
   int total_q;        // varlen: rows of the packed Q (row-wise kernels)
 };
 
