@@ -364,17 +364,26 @@ bwd_kernel(BwdParams p) {
 #endif
 
 // --------------------------------------------------------------------------
-// KV-outer kernel for head_dim 64 and 128: 8 waves = 4 key groups x 2 query halves.
+// KV-outer dK/dV kernel for head_dim 64 and 128 (the dQ kernel below runs first and
+// stores D = rowsum(dO * O)).
 //
-// A workgroup owns BN = 128 keys (wave w: keys 32*(w%4) .., query half w/4) and walks
-// query tiles of 64 rows; per tile each wave computes S/P/dP/dS for its 32 keys x 32
-// rows, accumulates dV^T += dO^T P and dK^T += Q^T dS in registers, stages dS^T in
-// LDS, and after a barrier computes one 32x32 block of dQ = dS K for the tile, added
-// to the fp32 accumulator with atomics.  K and V are read from swizzled LDS tiles
-// (B operands of S, dP and dQ).  Q/dO tiles are double-buffered in LDS through
-// direct buffer loads.  For causal attention a workgroup takes key tiles kt and
-// n-1-kt, so all workgroups do the same amount of work.  The two query halves'
-// dK/dV partials are summed in LDS.
+// A 4-wave workgroup owns BN = 64 keys of one KV head: wave w takes keys
+// 32*(w%2) .. +32 and query half w/2 of each 64-row query tile.  It walks every
+// (query head of the GQA group, query tile) item; per item each wave forms
+// S = Q K^T and dP = dO V^T for its 32 keys x 32 rows, P = exp2(S - L*log2e),
+// dS = P (dP - D), then dV^T += dO^T P and dK^T += Q^T dS in registers (Q^T, dO^T
+// read transposed from LDS, P and dS taken from the accumulators as B operands).
+//   - K is scaled by scale*log2e once per key tile, in LDS, and the S accumulator
+//     starts at -L*log2e, the dP accumulator at -D: the MFMAs produce the exponent
+//     and dP - D directly.
+//   - Operands of MFMA step t+1 are read before the MFMAs of step t.
+//   - Only tiles that straddle the diagonal apply the causal mask.
+//   - MFMA phases run at raised wave priority, so a SIMD's other wave fills their
+//     gaps rather than delaying them.
+// K/V tiles and the single-buffered Q/dO tile are staged in swizzled LDS by direct
+// buffer loads (66 KB, two workgroups per CU).  For causal attention a workgroup
+// takes key tiles kt and n-1-kt, so all workgroups do the same work.  The two query
+// halves' dK/dV partials are summed in LDS, in a fixed order.
 // --------------------------------------------------------------------------
 #ifndef FAL_BWD2_NW
 #define FAL_BWD2_NW 4   // waves per workgroup: 4 (64 keys, 2 workgroups per CU) or 8 (128 keys, double-buffered Q/dO)
@@ -507,6 +516,18 @@ bwd2_kernel(BwdParams p) {
       dk_acc[i] = zero_f16();
       dv_acc[i] = zero_f16();
     }
+    // K tile *= scale*log2e (in fp32, rounded once to fp16), so that S comes out of
+    // the MFMAs already in log2 units and the S accumulator can start at -L*log2e
+    wait_vmcnt0();
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPART / (NW * 64 * 8); ++i) {
+      half_t* ptr = ks_s + (i * NW * 64 + tid) * 8;
+      half8 v = load_h8(ptr);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] * c);
+      *reinterpret_cast<half8*>(ptr) = v;
+    }
     const int qt0 = CAUSAL ? (n0 / BMQ) : 0;
     // (query head, query tile) items of this key tile, in one sequence so the Q/dO
     // double buffer alternates across head boundaries too: the fetch of item it+1
@@ -537,16 +558,18 @@ bwd2_kernel(BwdParams p) {
         buffer_to_lds16(qrs, dl_offset(i, p.q_ss), qd_s + (buf * 2 + 0) * QPART + I * 64 * 8);
         buffer_to_lds16(dors, dl_offset(i, p.do_ss), qd_s + (buf * 2 + 1) * QPART + I * 64 * 8);
       }
+      // -L*log2e and -D, the initial values of the S and dP accumulators; a row
+      // past the end (or with no keys) gets -inf, so its P is 0
       if (tid < BMQ) {
-        float lv = INFINITY, dv = 0.f;
+        float nl = -INFINITY, nd = 0.f;
         if (q0 + tid < nq) {
           const int64_t o = (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)(q_off + q0 + tid) * p.l_ss;
           const float L = p.lse[o];
-          lv = (L == -INFINITY) ? INFINITY : L * kLog2e;
-          dv = p.delta[o];
+          nl = (L == -INFINITY) ? -INFINITY : -L * kLog2e;
+          nd = -p.delta[o];
         }
-        lpre = lv;
-        dpre = dv;
+        lpre = nl;
+        dpre = nd;
       }
     };
 
@@ -568,45 +591,86 @@ bwd2_kernel(BwdParams p) {
         const half_t* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
         const int qr0 = q0 + qh * 32;     // first query row of this wave's half
         if (!CAUSAL || qr0 + 31 >= kw0) {
-          // S = Q K^T and dP = dO V^T
-          f32x16 s = zero_f16(), dp = zero_f16();
+          // S = Q K^T - L*log2e and dP = dO V^T - D
+          f32x16 s, dp;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const f32x4 ln = *reinterpret_cast<const f32x4*>(&l_s[buf][qh * 32 + g4 * 8 + hh * 4]);
+            const f32x4 dn = *reinterpret_cast<const f32x4*>(&d_s[buf][qh * 32 + g4 * 8 + hh * 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              s[g4 * 4 + e] = ln[e];
+              dp[g4 * 4 + e] = dn[e];
+            }
+          }
+          __builtin_amdgcn_s_setprio(1);
+          // operands of step t+1 are read before the MFMAs of step t
+          const half_t* kw_s = ks_s + kg * 32 * CPR * 8;
+          const half_t* vw_s = vs_s + kg * 32 * CPR * 8;
+          half8 oq = load_h8(q_s + faddr(0)), ok = load_h8(kw_s + faddr(0));
+          half8 od = load_h8(do_s + faddr(0)), ov = load_h8(vw_s + faddr(0));
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            const int fa = faddr(t);
-            s = mfma32(load_h8(q_s + fa), load_h8(ks_s + fa + kg * 32 * CPR * 8), s);
-            dp = mfma32(load_h8(do_s + fa), load_h8(vs_s + fa + kg * 32 * CPR * 8), dp);
+            half8 nq, nk, nd, nv;
+            if (t + 1 < KS) {
+              const int fa = faddr(t + 1);
+              nq = load_h8(q_s + fa);
+              nk = load_h8(kw_s + fa);
+              nd = load_h8(do_s + fa);
+              nv = load_h8(vw_s + fa);
+            }
+            s = mfma32(oq, ok, s);
+            dp = mfma32(od, ov, dp);
             FAL_BWD_FENCE();
+            oq = nq; ok = nk; od = nd; ov = nv;
           }
-          // P and dS; element i: query qr0 + (i/4)*8 + hh*4 + i%4, key `key`.
+          __builtin_amdgcn_s_setprio(0);
+          // P = exp2(S) and dS = P dP; element i: query qr0 + (i/4)*8 + hh*4 + i%4, key `key`.
           // Query rows past the end carry L = +inf (P = 0), and keys past the end only
           // feed dK/dV rows that are never written, so the causal test is the only mask:
           // key > query  <=>  key - qr0 - hh*4 > (i/4)*8 + i%4, a constant per element.
           const int cthr = key - qr0 - hh * 4;
+          auto grad = [&](auto masked) {
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const f32x4 lv = *reinterpret_cast<const f32x4*>(&l_s[buf][qh * 32 + g4 * 8 + hh * 4]);
-            const f32x4 dv = *reinterpret_cast<const f32x4*>(&d_s[buf][qh * 32 + g4 * 8 + hh * 4]);
+            for (int g4 = 0; g4 < 4; ++g4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int i = g4 * 4 + e;
-              float pv = fast_exp2(fmaf(s[i], c, -lv[e]));
-              if (CAUSAL && cthr > g4 * 8 + e) pv = 0.f;
-              s[i] = pv;
-              dp[i] = pv * (dp[i] - dv[e]);
+              for (int e = 0; e < 4; ++e) {
+                const int i = g4 * 4 + e;
+                float pv = fast_exp2(s[i]);
+                if (decltype(masked)::value && cthr > g4 * 8 + e) pv = 0.f;
+                s[i] = pv;
+                dp[i] = pv * dp[i];
+              }
             }
-          }
+          };
+          // only a tile that straddles the diagonal has keys past some of its queries
+          if (CAUSAL && kw0 + 31 > qr0) grad(std::integral_constant<bool, true>{});
+          else grad(std::integral_constant<bool, false>{});
           // dV^T += dO^T P ; dK^T += Q^T dS
+          __builtin_amdgcn_s_setprio(1);
+          {
+            half8 pb[2], sb[2];
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const half8 pb = cvt8(s, ks);
-            const half8 sb = cvt8(dp, ks);
+            for (int ks = 0; ks < 2; ++ks) {
+              pb[ks] = cvt8(s, ks);
+              sb[ks] = cvt8(dp, ks);
+            }
+            half8 ao = trk(do_s, 0, 0), aq = trk(q_s, 0, 0);
 #pragma unroll
-            for (int db = 0; db < DWB; ++db) {
-              dv_acc[db] = mfma32(trk(do_s, db, ks * 16), pb, dv_acc[db]);
-              dk_acc[db] = mfma32(trk(q_s, db, ks * 16), sb, dk_acc[db]);
+            for (int st = 0; st < 2 * DWB; ++st) {
+              const int ks = st / DWB, db = st % DWB;
+              half8 no, nq;
+              if (st + 1 < 2 * DWB) {
+                no = trk(do_s, (st + 1) % DWB, (st + 1) / DWB * 16);
+                nq = trk(q_s, (st + 1) % DWB, (st + 1) / DWB * 16);
+              }
+              dv_acc[db] = mfma32(ao, pb[ks], dv_acc[db]);
+              dk_acc[db] = mfma32(aq, sb[ks], dk_acc[db]);
               FAL_BWD_FENCE();
+              ao = no; aq = nq;
             }
           }
+          __builtin_amdgcn_s_setprio(0);
         }
         if (!DBUF && item + 1 < nitems_q) {
           __syncthreads();                // barrier B: every wave is done with this item's tile
