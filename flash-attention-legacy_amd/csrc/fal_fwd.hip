@@ -39,6 +39,57 @@ namespace fal {
 #define FAL_FWD_KDEPTH 2
 #endif
 
+// A workgroup's (batch or sequence, query head, query tile) and its row ranges.
+struct FwdItem {
+  int b, hq, qt, q_off, k_off, nq, nk;
+};
+
+// Resolves the work item of this workgroup; false for a padding block, which exits.
+template <bool CAUSAL>
+__device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
+  if (p.cu_q) {
+    // 1-D grid over (work item, KV head) groups of G query heads.  Block i runs on XCD
+    // i % 8 as that XCD's (i / 8)-th block; the groups are dealt to the XCDs round-robin
+    // in work-list order (heaviest first), and the G heads of a group, which read the
+    // same K/V, run back to back on one XCD (one L2).  The grid is padded to a multiple
+    // of 8 groups; padding blocks exit.
+    const int g = p.Hq / p.Hkv;
+    const int k8 = blockIdx.x >> 3;
+    const int grp = (k8 / g) * 8 + (blockIdx.x & 7);
+    const int item = grp / p.Hkv;
+    if (item >= p.n_qtiles) return false;
+    const int2 wk = p.work[item];
+    if (wk.x < 0) return false;
+    it.hq = (grp % p.Hkv) * g + k8 % g;
+    it.b = 0;
+    it.qt = wk.y;
+    it.q_off = p.cu_q[wk.x];
+    it.nq = p.cu_q[wk.x + 1] - it.q_off;
+    it.k_off = p.cu_k[wk.x];
+    it.nk = p.cu_k[wk.x + 1] - it.k_off;
+  } else {
+    // 1-D grid; group heads of one KV head and the query tiles of a head together so the
+    // workgroups an XCD runs at once share K/V in that XCD's L2 (workgroups are dealt to
+    // the 8 XCDs round-robin by linear id).
+    const int total = gridDim.x;
+    int id = blockIdx.x;
+    if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+    const int g = p.Hq / p.Hkv;
+    const int hg = id % g;
+    int rest = id / g;
+    const int t = rest % p.n_qtiles;
+    rest /= p.n_qtiles;                          // = b * Hkv + hkv
+    it.qt = CAUSAL ? (p.n_qtiles - 1 - t) : t;   // heaviest causal tiles first
+    it.b = rest / p.Hkv;
+    it.hq = (rest % p.Hkv) * g + hg;
+    it.q_off = 0;
+    it.k_off = 0;
+    it.nq = p.Nq;
+    it.nk = p.Nk;
+  }
+  return true;
+}
+
 template <int D, int NW, int BN, bool CAUSAL, int RB>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(RB == 2 ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
@@ -62,47 +113,9 @@ fwd_kernel(FwdParams p) {
   const int hh = lane >> 5;
 
   // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
-  int b, hq, qt, q_off, k_off, nq, nk;
-  if (p.cu_q) {
-    // 1-D grid over (work item, KV head) groups of G query heads.  Block i runs on XCD
-    // i % 8 as that XCD's (i / 8)-th block; the groups are dealt to the XCDs round-robin
-    // in work-list order (heaviest first), and the G heads of a group, which read the
-    // same K/V, run back to back on one XCD (one L2).  The grid is padded to a multiple
-    // of 8 groups; padding blocks exit.
-    const int g = p.Hq / p.Hkv;
-    const int k8 = blockIdx.x >> 3;
-    const int grp = (k8 / g) * 8 + (blockIdx.x & 7);
-    const int item = grp / p.Hkv;
-    if (item >= p.n_qtiles) return;
-    const int2 wk = p.work[item];
-    if (wk.x < 0) return;
-    hq = (grp % p.Hkv) * g + k8 % g;
-    b = 0;
-    qt = wk.y;
-    q_off = p.cu_q[wk.x];
-    nq = p.cu_q[wk.x + 1] - q_off;
-    k_off = p.cu_k[wk.x];
-    nk = p.cu_k[wk.x + 1] - k_off;
-  } else {
-    // 1-D grid; group heads of one KV head and the query tiles of a head together so the
-    // workgroups an XCD runs at once share K/V in that XCD's L2 (workgroups are dealt to
-    // the 8 XCDs round-robin by linear id).
-    const int total = gridDim.x;
-    int id = blockIdx.x;
-    if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
-    const int g = p.Hq / p.Hkv;
-    const int hg = id % g;
-    int rest = id / g;
-    const int t = rest % p.n_qtiles;
-    rest /= p.n_qtiles;                       // = b * Hkv + hkv
-    qt = CAUSAL ? (p.n_qtiles - 1 - t) : t;   // heaviest causal tiles first
-    b = rest / p.Hkv;
-    hq = (rest % p.Hkv) * g + hg;
-    q_off = 0;
-    k_off = 0;
-    nq = p.Nq;
-    nk = p.Nk;
-  }
+  FwdItem it;
+  if (!fwd_item<CAUSAL>(p, it)) return;
+  const int b = it.b, hq = it.hq, qt = it.qt, q_off = it.q_off, k_off = it.k_off, nq = it.nq, nk = it.nk;
   const int hkv = hq / (p.Hq / p.Hkv);
   const int m0 = qt * BM;
   if (m0 >= nq) return;
