@@ -175,7 +175,8 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
   int nb = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
   nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, bm, nb, is_causal ? 1 : 0, work, cap, st);
+  hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nb, is_causal ? 1 : 0, work,
+                                        cap, st);
   if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
 
   FwdParams p{};
@@ -192,6 +193,8 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
   p.B = 1; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
   p.scale_log2 = signed_scale_log2(softmax_scale);
   p.cu_q = cu_seqlens_q;
+  p.total_q = (int)total_q;
+  p.total_k = (int)total_k;
   p.cu_k = cu_seqlens_k;
   p.work = work;
   p.n_qtiles = cap;   // work-list capacity
@@ -359,6 +362,7 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
   p.l_sb = 0; p.l_sh = 1; p.l_ss = heads_q;
   p.B = 1; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
   p.total_q = (int)total_q;
+  p.total_k = (int)total_k;
   p.scale = softmax_scale;
   p.scale_log2 = softmax_scale * kLog2e;
   p.cu_q = cu_seqlens_q;
@@ -371,7 +375,7 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
   // Every key row of every segment is covered by exactly one work item, which writes
   // its dK/dV rows (zeros when the segment has no query rows).  Rows outside all
   // segments are not written; the caller pre-zeroes dk/dv if it needs them defined.
-  hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, bn, nb, 0, work, cap, st);
+  hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, (int)total_k, bn, nb, 0, work, cap, st);
   if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen schedule");
   dim3 dq_grid(0, 0);
   if (bwd_split_dq((int)head_dim)) {
@@ -381,7 +385,8 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
     int2* qwork = work + align256((size_t)cap * sizeof(int2)) / sizeof(int2);
     int nbq = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
     nbq = nbq < 1 ? 1 : (nbq > 8192 ? 8192 : nbq);
-    e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, bm, nbq, is_causal ? 1 : 0, qwork, capq, st);
+    e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nbq, is_causal ? 1 : 0, qwork,
+                               capq, st);
     if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen dq schedule");
     p.qwork = qwork;
     p.n_qitems = capq;
@@ -443,6 +448,7 @@ int fal_decode(const void* q, const void* k_cache, const void* v_cache, const in
   p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
   p.o_sb = o_strides[0]; p.o_sh = o_strides[1];
   p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
+  p.max_seqlen = (int)max_seqlen_k;
   p.chunk = decode_chunk((int)head_dim, (int)batch, (int)heads_kv, (int)(max_seqlen_k > 0 ? max_seqlen_k : 1));
   p.max_splits = cdiv((int)(max_seqlen_k > 0 ? max_seqlen_k : 1), p.chunk);
   const size_t parts = (size_t)batch * heads_q * p.max_splits;

@@ -145,10 +145,8 @@ bwd_kernel(BwdParams p) {
     hkv = blockIdx.y;
     b = 0;
     kt = wk.y;
-    q_off = p.cu_q[wk.x];
-    nq = p.cu_q[wk.x + 1] - q_off;
-    k_off = p.cu_k[wk.x];
-    nk = p.cu_k[wk.x + 1] - k_off;
+    seg_bounds(p.cu_q, wk.x, p.total_q, q_off, nq);
+    seg_bounds(p.cu_k, wk.x, p.total_k, k_off, nk);
   } else {
     const int total = gridDim.x;
     int id = blockIdx.x;
@@ -429,10 +427,8 @@ bwd2_kernel(BwdParams p) {
     b = 0;
     kt_a = wk.y;
     kt_b = -1;
-    q_off = p.cu_q[wk.x];
-    nq = p.cu_q[wk.x + 1] - q_off;
-    k_off = p.cu_k[wk.x];
-    nk = p.cu_k[wk.x + 1] - k_off;
+    seg_bounds(p.cu_q, wk.x, p.total_q, q_off, nq);
+    seg_bounds(p.cu_k, wk.x, p.total_k, k_off, nk);
   } else {
     const int total = gridDim.x;
     int id = blockIdx.x;
@@ -768,10 +764,8 @@ bwd_dq_kernel(BwdParams p) {
     hq = (grp % p.Hkv) * g + k8 % g;
     b = 0;
     qt_a = wk.y;
-    q_off = p.cu_q[wk.x];
-    nq = p.cu_q[wk.x + 1] - q_off;
-    k_off = p.cu_k[wk.x];
-    nk = p.cu_k[wk.x + 1] - k_off;
+    seg_bounds(p.cu_q, wk.x, p.total_q, q_off, nq);
+    seg_bounds(p.cu_k, wk.x, p.total_k, k_off, nk);
   } else {
     // heads of one KV head and the query tiles of a head are dealt to one XCD together
     const int total = gridDim.x;

@@ -133,6 +133,16 @@ __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rs, int v
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds_wave_base), 16,
                                            voffset, 0, 0, AUX);
 }
+// Segment s of a cu_seqlens array, clamped to [0, total): a malformed array (not
+// monotone, or past the packed tensor) yields empty or shortened segments, never
+// rows outside the tensor.
+__device__ __forceinline__ void seg_bounds(const int* cu, int s, int total, int& off, int& len) {
+  const int a = min(max(cu[s], 0), total);
+  const int e = min(max(cu[s + 1], a), total);
+  off = a;
+  len = e - a;
+}
+
 __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Row-major LDS tile of D fp16 columns stored as 16-byte chunks with an XOR swizzle

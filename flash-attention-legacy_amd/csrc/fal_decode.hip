@@ -85,7 +85,7 @@ decode_split_kernel(DecodeParams p) {
   const int split = wk.y;
   const int hkv = (blockIdx.x % heads_tiles) / nhg;
   const int hg = (blockIdx.x % heads_tiles) % nhg;
-  const int L = p.seqlens[b];
+  const int L = min(max(p.seqlens[b], 0), p.max_seqlen);
   const int k_begin = split * p.chunk;
   if (k_begin >= L) return;
   const int k_end = min(L, k_begin + p.chunk);
@@ -271,7 +271,7 @@ decode_combine_kernel(DecodeParams p) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
   const int lane = threadIdx.x;
-  const int L = p.seqlens[b];
+  const int L = min(max(p.seqlens[b], 0), p.max_seqlen);
   const int ns = cdiv(max(L, 0), p.chunk);
   const int64_t base = ((int64_t)b * p.Hq + hq) * p.max_splits;
   constexpr int DJ = (D + 63) / 64;
@@ -332,13 +332,14 @@ decode_combine_kernel(DecodeParams p) {
 // start first, so the kernel does not end on a tail of long splits.  Built on the
 // device from cache_seqlens; unused trailing slots get (-1, -1).
 __global__ void __launch_bounds__(1024)
-decode_schedule_kernel(const int* __restrict__ seqlens, int B, int chunk, int2* __restrict__ work, int capacity) {
+decode_schedule_kernel(const int* __restrict__ seqlens, int B, int max_seqlen, int chunk, int2* __restrict__ work,
+                       int capacity) {
   __shared__ int hist[64], cur[64], full_total, full_cur;
   for (int i = threadIdx.x; i < 64; i += blockDim.x) hist[i] = 0;
   if (threadIdx.x == 0) full_total = 0;
   __syncthreads();
   for (int b = threadIdx.x; b < B; b += blockDim.x) {
-    const int L = max(seqlens[b], 0);
+    const int L = min(max(seqlens[b], 0), max_seqlen);
     if (L / chunk) atomicAdd(&full_total, L / chunk);
     if (L % chunk) atomicAdd(&hist[(L % chunk) * 64 / chunk], 1);
   }
@@ -355,7 +356,7 @@ decode_schedule_kernel(const int* __restrict__ seqlens, int B, int chunk, int2* 
   __syncthreads();
   const int total = hist[0];
   for (int b = threadIdx.x; b < B; b += blockDim.x) {
-    const int L = max(seqlens[b], 0);
+    const int L = min(max(seqlens[b], 0), max_seqlen);
     const int nf = L / chunk;
     if (nf) {
       const int pos = atomicAdd(&full_cur, nf);
@@ -382,7 +383,7 @@ template <int D>
 static hipError_t launch_decode_d(const DecodeParams& p, hipStream_t st) {
   const int nhg = cdiv(p.Hq / p.Hkv, 16);
   const int capacity = p.B * p.max_splits;
-  hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(1024), 0, st, p.seqlens, p.B, p.chunk,
+  hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(1024), 0, st, p.seqlens, p.B, p.max_seqlen, p.chunk,
                      const_cast<int2*>(p.work), capacity);
   hipError_t e0 = hipGetLastError();
   if (e0 != hipSuccess) return e0;

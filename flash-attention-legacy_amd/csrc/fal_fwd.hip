@@ -63,10 +63,8 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
     it.hq = (grp % p.Hkv) * g + k8 % g;
     it.b = 0;
     it.qt = wk.y;
-    it.q_off = p.cu_q[wk.x];
-    it.nq = p.cu_q[wk.x + 1] - it.q_off;
-    it.k_off = p.cu_k[wk.x];
-    it.nk = p.cu_k[wk.x + 1] - it.k_off;
+    seg_bounds(p.cu_q, wk.x, p.total_q, it.q_off, it.nq);
+    seg_bounds(p.cu_k, wk.x, p.total_k, it.k_off, it.nk);
   } else {
     // 1-D grid; group heads of one KV head and the query tiles of a head together so the
     // workgroups an XCD runs at once share K/V in that XCD's L2 (workgroups are dealt to
@@ -398,7 +396,7 @@ fwd_kernel(FwdParams p) {
 // (descending=0).  Unused trailing slots get (-1, -1).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
-varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int tile, int nbuckets,
+varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int tile, int nbuckets,
                        int descending, int2* __restrict__ work, int capacity) {
   extern __shared__ int sh[];            // [nbuckets] counts, then [nbuckets] cursors
   int* cnt = sh;
@@ -406,7 +404,9 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int tile, int n
   for (int i = threadIdx.x; i < nbuckets; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
   for (int s = threadIdx.x; s < num_seqs; s += blockDim.x) {
-    const int nt = cdiv(max(cu[s + 1] - cu[s], 0), tile);
+    int off, len;
+    seg_bounds(cu, s, rows, off, len);
+    const int nt = cdiv(len, tile);
     for (int t = 0; t < nt; ++t) atomicAdd(&cnt[min(t, nbuckets - 1)], 1);
   }
   __syncthreads();
@@ -422,7 +422,9 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int tile, int n
   __syncthreads();
   const int total = cnt[0];
   for (int s = threadIdx.x; s < num_seqs; s += blockDim.x) {
-    const int nt = cdiv(max(cu[s + 1] - cu[s], 0), tile);
+    int off, len;
+    seg_bounds(cu, s, rows, off, len);
+    const int nt = cdiv(len, tile);
     for (int t = 0; t < nt; ++t) {
       const int pos = atomicAdd(&cur[min(t, nbuckets - 1)], 1);
       if (pos < capacity) work[pos] = make_int2(s, t);
@@ -475,10 +477,10 @@ hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStrea
   }
 }
 
-hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int tile, int nbuckets, int descending,
+hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int rows, int tile, int nbuckets, int descending,
                                   int2* work, int capacity, hipStream_t st) {
   const size_t shmem = 2 * sizeof(int) * (size_t)nbuckets;
-  hipLaunchKernelGGL(varlen_schedule_kernel, dim3(1), dim3(1024), shmem, st, cu, num_seqs, tile,
+  hipLaunchKernelGGL(varlen_schedule_kernel, dim3(1), dim3(1024), shmem, st, cu, num_seqs, rows, tile,
                      nbuckets, descending, work, capacity);
   return hipGetLastError();
 }

@@ -25,6 +25,7 @@ struct FwdParams {
   int64_t l_sb, l_sh, l_ss;
   int B, Hq, Hkv, Nq, Nk;
   int n_qtiles;
+  int total_q, total_k;   // varlen: rows of the packed Q and K/V (segments are clamped to them)
   float scale_log2;   // softmax_scale * log2(e), signed, |.| >= 1e-30
   const int* cu_q;
   const int* cu_k;
@@ -66,6 +67,7 @@ struct BwdParams {
   const int2* qwork;  // (sequence, query-tile) list of the dQ kernel in varlen mode
   int n_qitems;       // capacity of qwork
   int total_q;        // varlen: rows of the packed Q (row-wise kernels)
+  int total_k;        // varlen: rows of the packed K/V
 };
 
 // KV-cache decode (one query token per sequence).
@@ -86,13 +88,14 @@ struct DecodeParams {
   int64_t o_sb, o_sh;
   int64_t bias_sb;
   int B, Hq, Hkv, max_splits, chunk;
+  int max_seqlen;           // cache rows; cache_seqlens are clamped to it
   float scale_log2;
   int negate_q;
 };
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 int fwd_block_m(int d);
-hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int tile, int nbuckets, int descending,
+hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int rows, int tile, int nbuckets, int descending,
                                   int2* work, int capacity, hipStream_t st);
 
 int bwd_block_n(int d);

@@ -130,3 +130,15 @@ def test_decode_deterministic():
     for _ in range(5):
         o, l = hip_ext.decode(q, kc, vc, seq, 0.088, return_lse=True)
         assert torch.equal(o, o0) and torch.equal(l, l0)
+
+
+def test_cache_seqlens_beyond_capacity_are_clamped():
+    """cache_seqlens above the cache capacity (or negative) behave as the lengths
+    clamped to [0, S]: the kernels clamp on the device and never read past the cache
+    or write past the workspace."""
+    B, hq, hkv, S, d = 3, 8, 2, 64, 128
+    q = randn((B, hq, d), seed=50)
+    kc, vc = randn((B, S, hkv, d), seed=51), randn((B, S, hkv, d), seed=52)
+    o_g, l_g = run(q, kc, vc, [S, 5, 0], 0.088, lse=True)
+    o_b, l_b = run(q, kc, vc, [S + 1000, 5, -3], 0.088, lse=True)
+    assert torch.equal(o_g, o_b) and torch.equal(l_g, l_b)

@@ -128,3 +128,27 @@ def test_config_c4_forward():
             vi = v[c[i]:c[i + 1], g:g + 1].permute(1, 0, 2)[None].cpu()
             ref = ref_attention(qi, ki, vi, scale, True)[0].permute(1, 0, 2)
             assert max_abs(o[c[i]:c[i + 1], hs], ref) <= FWD_ATOL, (i, g)
+
+
+@pytest.mark.parametrize("d", [96, 128])
+def test_malformed_cu_seqlens_are_clamped(d):
+    """A cu_seqlens array past the packed tensor (last entry total + 50, a second
+    entry beyond it too) behaves as the array clamped to [0, total]: the kernels
+    clamp every segment on the device, so no row outside the tensor is touched.
+    Forward and backward must equal the well-formed call bit for bit."""
+    from flash_attn_legacy import hip_ext
+    lens = [100, 157]
+    total = sum(lens)
+    q, k, v = randn((total, 4, d), seed=40), randn((total, 2, d), seed=41), randn((total, 2, d), seed=42)
+    do = randn((total, 4, d), seed=43)
+    good = cu_from_lens(lens)
+    bad = torch.tensor([0, 100, total + 50], dtype=torch.int32, device="cuda")
+    scale = 1.0 / math.sqrt(d)
+    for causal in (False, True):
+        o_g, l_g = hip_ext.forward_varlen(q, k, v, good, good, max(lens), max(lens), scale, causal)
+        o_b, l_b = hip_ext.forward_varlen(q, k, v, bad, bad, 207, 207, scale, causal)
+        assert torch.equal(o_g, o_b) and torch.equal(l_g, l_b)
+        g_g = hip_ext.backward_varlen(do, q, k, v, o_g, l_g, good, good, max(lens), max(lens), scale, causal)
+        g_b = hip_ext.backward_varlen(do, q, k, v, o_g, l_g, bad, bad, 207, 207, scale, causal)
+        for a, b in zip(g_g, g_b):
+            assert torch.equal(a, b)
