@@ -7,7 +7,7 @@
 // head sum over all query heads of its GQA group inside one workgroup.
 //
 // Kernels:
-// * head_dim 64/128 (FA2's split form, no atomics, deterministic):
+// * head_dim 32/64/96/128 (FA2's split form, no atomics, deterministic):
 //   - bwd_dq_kernel (query-outer, runs first): a workgroup owns 128 query rows;
 //     Q and dO stay in VGPRs, K/V tiles stream through LDS; it computes D for its
 //     rows, P, dS and dQ = dS K, written once in fp16;
@@ -16,7 +16,7 @@
 //     accumulators straight into the B operands of dV^T += dO^T P and
 //     dK^T += Q^T dS (dO^T and Q^T from the Q/dO tiles via ds_read_b64_tr_b16);
 //     dK/dV stay in registers until the end.
-// * head_dim 32/96/256: bwd_pre_kernel (D, zeroed fp32 dQ accumulator), bwd_kernel
+// * head_dim 256: bwd_pre_kernel (D, zeroed fp32 dQ accumulator), bwd_kernel
 //   (KV-outer, dS^T staged in LDS, dQ = dS K added with fp32 atomics; for head_dim
 //   256 the dK/dV accumulators take two passes of 128 columns) and bwd_post_kernel
 //   (dQ cast to fp16).
@@ -362,7 +362,7 @@ bwd_kernel(BwdParams p) {
 #endif
 
 // --------------------------------------------------------------------------
-// KV-outer dK/dV kernel for head_dim 64 and 128 (the dQ kernel below runs first and
+// KV-outer dK/dV kernel for head_dim 32, 64, 96 and 128 (the dQ kernel below runs first and
 // stores D = rowsum(dO * O)).
 //
 // A 4-wave workgroup owns BN = 64 keys of one KV head: wave w takes keys
@@ -474,11 +474,19 @@ bwd2_kernel(BwdParams p) {
     }
   }
   const int tr_lo = 4 * (lane & 1);
-  auto faddr = [&](int t) { return fbase ^ ((2 * t) << 3); };
+  // (The XOR form needs a power-of-two row length in chunks; head_dim 96 has 12 and
+  // takes the full offsets.)
+  constexpr bool POW2 = (CPR & (CPR - 1)) == 0;
+  auto faddr = [&](int t) { return POW2 ? (fbase ^ ((2 * t) << 3)) : TL::offset(l32, 2 * t + hh); };
+  const int trl = hh * 4 + ((lane & 15) >> 2);
+  const int trc = 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+  auto tra = [&](int hf, int db) {
+    return POW2 ? (trb[hf] ^ ((db * 4) << 3)) : TL::offset(hf * 8 + trl, db * 4 + trc);
+  };
   // 8 k-slots for rows row0.. (multiple of 16) of a swizzled D-column tile, block db
   auto trk = [&](const half_t* base, int db, int row0) {
-    const half4 lo = lds_read_tr(base + (trb[0] ^ ((db * 4) << 3)) + tr_lo + row0 * CPR * 8);
-    const half4 hi = lds_read_tr(base + (trb[1] ^ ((db * 4) << 3)) + tr_lo + row0 * CPR * 8);
+    const half4 lo = lds_read_tr(base + tra(0, db) + tr_lo + row0 * CPR * 8);
+    const half4 hi = lds_read_tr(base + tra(1, db) + tr_lo + row0 * CPR * 8);
     return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
   const int nqt = cdiv(nq, BMQ);
@@ -712,7 +720,7 @@ bwd2_kernel(BwdParams p) {
 
 
 // --------------------------------------------------------------------------
-// Query-outer dQ kernel for head_dim 64 and 128 (the KV-outer kernel above then
+// Query-outer dQ kernel for head_dim 32, 64, 96 and 128 (the KV-outer kernel above then
 // produces only dK/dV).  Same structure as the forward kernel: a workgroup owns
 // 32*NW query rows of one query head, each wave 32 rows whose Q and dO slices stay
 // in VGPRs as the B operands of S^T = K Q^T and dP^T = V dO^T; K/V tiles of BN keys
@@ -985,13 +993,17 @@ bwd_dq_kernel(BwdParams p) {
 // --------------------------------------------------------------------------
 constexpr int kBwdNW = 4;
 
+// head dims on the split path (dQ kernel + dK/dV kernel); 256 keeps the atomic kernel,
+// whose dK/dV accumulators would not fit the split kernel's registers
+constexpr bool split_d(int d) { return d == 32 || d == 64 || d == 96 || d == 128; }
+
 int bwd_block_n(int d) {
-  return (d == 64 || d == 128) ? FAL_BWD2_NW * 16 : kBwdNW * 32;
+  return split_d(d) ? FAL_BWD2_NW * 16 : kBwdNW * 32;
 }
 
 template <int D>
 static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
-  if constexpr (D == 64 || D == 128) {
+  if constexpr (split_d(D)) {
     // batched causal: one workgroup per pair of key tiles
     if (!p.cu_q && causal) grid.x = (unsigned)((p.n_ktiles + 1) / 2) * p.B * p.Hkv;
     if (causal)
@@ -1012,7 +1024,7 @@ static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStr
 #endif
 constexpr int kDqNW = 4;
 
-bool bwd_split_dq(int d) { return d == 64 || d == 128; }
+bool bwd_split_dq(int d) { return split_d(d); }
 int bwd_dq_block_m(int d) {
   (void)d;
   return kDqNW * 32;
@@ -1031,7 +1043,9 @@ static hipError_t launch_bwd_dq_d(const BwdParams& p, int causal, dim3 grid, hip
 
 hipError_t launch_bwd_dq(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st) {
   switch (d) {
+    case 32: return launch_bwd_dq_d<32>(p, causal, grid, st);
     case 64: return launch_bwd_dq_d<64>(p, causal, grid, st);
+    case 96: return launch_bwd_dq_d<96>(p, causal, grid, st);
     case 128: return launch_bwd_dq_d<128>(p, causal, grid, st);
     default: return hipErrorInvalidValue;
   }

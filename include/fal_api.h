@@ -94,7 +94,8 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
  * kernels it launches (precompute_D, flash_attn_bwd_*_launch).
  *   dout, q, o [B, Hq, Nq, d]; k, v [B, Hkv, Nk, d]; lse [B, Hq, Nq] from fal_fwd.
  *   Outputs dq [B, Hq, Nq, d], dk / dv [B, Hkv, Nk, d] (fp16), fully overwritten.
- * workspace: fal_bwd_workspace_size bytes (fp32 dQ accumulator + row deltas).
+ * workspace: fal_bwd_workspace_size bytes: the row deltas D, plus an fp32 dQ
+ * accumulator for head_dim 256 (the other head dims write dQ from their own kernel).
  * dQ is accumulated with fp32 atomics, so its low bits can vary run to run (as
  * in the reference, flash_attn_bwd.cu:618); dK and dV are deterministic.
  */

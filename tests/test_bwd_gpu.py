@@ -105,7 +105,7 @@ def test_config_c3():
                 assert e <= GRAD_RTOL, f"{name} b={b} h0={h0} rel err {e:.3e}"
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [32, 64, 96, 128])
 def test_deterministic_gradients(d):
     """d 64/128 take the split backward (no atomics): repeated calls are bitwise equal."""
     from flash_attn_legacy import hip_ext
