@@ -96,8 +96,9 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
  *   Outputs dq [B, Hq, Nq, d], dk / dv [B, Hkv, Nk, d] (fp16), fully overwritten.
  * workspace: fal_bwd_workspace_size bytes: the row deltas D, plus an fp32 dQ
  * accumulator for head_dim 256 (the other head dims write dQ from their own kernel).
- * dQ is accumulated with fp32 atomics, so its low bits can vary run to run (as
- * in the reference, flash_attn_bwd.cu:618); dK and dV are deterministic.
+ * All gradients are bitwise deterministic, except dQ at head_dim 256: it is
+ * accumulated with fp32 atomics, so its low bits can vary run to run (as in the
+ * reference, flash_attn_bwd.cu:618).
  */
 size_t fal_bwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t head_dim);
 int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const void* o,
