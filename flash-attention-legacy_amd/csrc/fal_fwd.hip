@@ -90,7 +90,7 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
 
 template <int D, int NW, int BN, bool CAUSAL, int RB>
 __global__ void __launch_bounds__(NW * 64)
-__attribute__((amdgpu_waves_per_eu(RB == 2 ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
+__attribute__((amdgpu_waves_per_eu((RB == 2 && D >= 128) ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
 fwd_kernel(FwdParams p) {
   using TL = SwizzledTile<D>;
   constexpr int BM = NW * 32 * RB;  // query rows per workgroup (RB 32-row blocks per wave)
@@ -442,11 +442,23 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
 #ifndef FAL_FWD_NW128
 #define FAL_FWD_NW128 4   // waves per workgroup for head_dim 128
 #endif
+#ifndef FAL_FWD_BN32
+#define FAL_FWD_BN32 128   // head_dim 32: 128-key tiles (+25% causal, +3% non-causal over 64)
+#endif
+#ifndef FAL_FWD_BN64
+#define FAL_FWD_BN64 FAL_FWD_BN
+#endif
+#ifndef FAL_FWD_RB32
+#define FAL_FWD_RB32 1
+#endif
+#ifndef FAL_FWD_RB64
+#define FAL_FWD_RB64 1
+#endif
 template <int D>
 struct FwdCfg {
   static constexpr int NW = D == 128 ? FAL_FWD_NW128 : 4;
-  static constexpr int BN = (D >= 256) ? 32 : FAL_FWD_BN;
-  static constexpr int RB = (D == 128) ? FAL_FWD_RB128 : 1;
+  static constexpr int BN = (D >= 256) ? 32 : D == 32 ? FAL_FWD_BN32 : D == 64 ? FAL_FWD_BN64 : FAL_FWD_BN;
+  static constexpr int RB = D == 128 ? FAL_FWD_RB128 : D == 32 ? FAL_FWD_RB32 : D == 64 ? FAL_FWD_RB64 : 1;
 };
 
 template <int D>
@@ -459,10 +471,16 @@ static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStr
   return hipGetLastError();
 }
 
+template <int D>
+constexpr int fwd_bm() { return FwdCfg<D>::NW * 32 * FwdCfg<D>::RB; }
+
 int fwd_block_m(int d) {
   switch (d) {
-    case 128: return FwdCfg<128>::NW * 32 * FwdCfg<128>::RB;
-    default: return 4 * 32;
+    case 32: return fwd_bm<32>();
+    case 64: return fwd_bm<64>();
+    case 96: return fwd_bm<96>();
+    case 128: return fwd_bm<128>();
+    default: return fwd_bm<256>();
   }
 }
 
