@@ -8,10 +8,12 @@ TestForwardGQA :145-193, TestLongSequences :486-547, TestNumericalStability
 
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
-from helpers import FWD_ATOL, max_abs, oracle_fwd, randn
+from helpers import FWD_ATOL, max_abs, np64, oracle_fwd, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -206,3 +208,36 @@ def test_config_c2_full_shape():
             ref = ref_attention(q[b:b + 1, hs].cpu(), k[b:b + 1, g:g + 1].cpu(), v[b:b + 1, g:g + 1].cpu(),
                                 scale, True)
             assert max_abs(o[b:b + 1, hs], ref) <= FWD_ATOL, (b, g)
+
+
+def exact_rows(q, k, v, rows, scale, causal):
+    """float64 attention output and log-sum-exp (natural log) of the given query rows of
+    one head (q [Nq, d], k/v [Nk, d]), the closed form of oracle/attention.py one row
+    at a time, with top-left causal alignment."""
+    qf, kf, vf = (np64(t) for t in (q, k, v))
+    outs, lses = [], []
+    for r in rows:
+        kk = kf[: r + 1] if causal else kf
+        vv = vf[: r + 1] if causal else vf
+        s = kk @ qf[r] * scale
+        m = s.max()
+        p = np.exp(s - m)
+        outs.append(p @ vv / p.sum())
+        lses.append(m + np.log(p.sum()))
+    return np.stack(outs), np.array(lses)
+
+
+@pytest.mark.parametrize("causal,nq,nk", [(True, 32768, 32768), (False, 4000, 32768)])
+def test_very_long_sequence_sampled_rows(causal, nq, nk):
+    """N up to 32768 (beyond the dense oracle's reach): O and L of sampled rows, first,
+    middle and last, against exact float64 rows; GQA with 2 query heads per KV head."""
+    Hq, Hkv, d = 2, 1, 128
+    q = randn((1, Hq, nq, d), seed=60)
+    k, v = randn((1, Hkv, nk, d), seed=61), randn((1, Hkv, nk, d), seed=62)
+    scale = 1.0 / math.sqrt(d)
+    o, lse = ext().forward(q, k, v, scale, causal)
+    rows = [0, 1, 63, 64, nq // 2 - 1, nq // 2 + 17, nq - 2, nq - 1]
+    for h in range(Hq):
+        ref_o, ref_l = exact_rows(q[0, h], k[0, 0], v[0, 0], rows, scale, causal)
+        assert max_abs(o[0, h, rows], torch.from_numpy(ref_o)) <= FWD_ATOL, h
+        assert float(np.abs(lse[0, h, rows].cpu().numpy() - ref_l).max()) <= 1e-3, h
