@@ -9,10 +9,12 @@ max|g - g_ref| / max|g_ref| <= 1e-2 per gradient against the fp64 oracle
 
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
-from helpers import GRAD_RTOL, oracle_bwd, randn, rel_err
+from helpers import GRAD_RTOL, np64, oracle_bwd, randn, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -116,3 +118,51 @@ def test_deterministic_gradients(d):
         g = hip_ext.backward(do, q, k, v, o, lse, 0.1, True)
         for a, b in zip(g, g0):
             assert torch.equal(a, b)
+
+
+def test_long_sequence_sampled_gradients():
+    """N = 16384, causal, 2 query heads per KV head: sampled rows of dQ against float64
+    rows computed from that row alone (O, L, D, P, dP, dS over all its keys), and
+    sampled rows of dK / dV against float64 sums over every query row that sees the key
+    (those sums take each row's L and D from the kernel's forward L and O, whose sampled
+    rows are themselves checked in test_fwd_gpu.py)."""
+    from flash_attn_legacy import hip_ext
+    Hq, Hkv, N, d = 2, 1, 16384, 128
+    scale = 1.0 / math.sqrt(d)
+    q = randn((1, Hq, N, d), seed=70)
+    k, v = randn((1, Hkv, N, d), seed=71), randn((1, Hkv, N, d), seed=72)
+    do = randn((1, Hq, N, d), seed=73)
+    o, lse = hip_ext.forward(q, k, v, scale, True)
+    dq, dk, dv = hip_ext.backward(do, q, k, v, o, lse, scale, True)
+    qf, kf, vf, dof, of = (np64(t)[0] for t in (q, k, v, do, o))
+    lf = lse[0].double().cpu().numpy()
+    kk, vv = kf[0], vf[0]
+    rows = [0, 5, 4095, 8191, 12000, N - 1]
+    for h in range(Hq):
+        ref = []
+        for r in rows:
+            s = kk[: r + 1] @ qf[h, r] * scale
+            m = s.max()
+            p = np.exp(s - m)
+            L = m + np.log(p.sum())
+            p = np.exp(s - L)
+            orow = p @ vv[: r + 1]
+            dp = vv[: r + 1] @ dof[h, r]
+            ds = p * (dp - dof[h, r] @ orow)
+            ref.append(scale * ds @ kk[: r + 1])
+        assert rel_err(dq[0, h, rows], torch.from_numpy(np.stack(ref))) <= GRAD_RTOL, h
+    keys = [0, 7, 4096, 10000, N - 2, N - 1]
+    dk_ref, dv_ref = [], []
+    for j in keys:
+        gk, gv = np.zeros(d), np.zeros(d)
+        for h in range(Hq):
+            qq, gg = qf[h, j:], dof[h, j:]
+            p = np.exp(qq @ kk[j] * scale - lf[h, j:])
+            dp = gg @ vv[j]
+            dd = np.einsum("rd,rd->r", gg, of[h, j:])
+            gk += scale * (p * (dp - dd)) @ qq
+            gv += p @ gg
+        dk_ref.append(gk)
+        dv_ref.append(gv)
+    assert rel_err(dk[0, 0, keys], torch.from_numpy(np.stack(dk_ref))) <= GRAD_RTOL
+    assert rel_err(dv[0, 0, keys], torch.from_numpy(np.stack(dv_ref))) <= GRAD_RTOL
