@@ -39,7 +39,7 @@ _I64 = ctypes.c_int64
 _F32 = ctypes.c_float
 _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
-_STR = ctypes.POINTER(ctypes.c_int64)
+_STR = ctypes.c_void_p   # int64[3] stride triples, passed as arrays or byref(array, offset)
 
 
 def _load() -> ctypes.CDLL:
@@ -103,12 +103,37 @@ def _strides(t: torch.Tensor, dims=(0, 1, 2)):
     return (ctypes.c_int64 * 3)(*[s[i] if i is not None else 0 for i in dims])
 
 
+def _stride_block(*ts: torch.Tensor):
+    """The (batch, head, sequence) strides of 4-D tensors in one ctypes array, and a
+    pointer to each tensor's triple (one allocation instead of one per tensor)."""
+    vals = []
+    for t in ts:
+        vals.extend(t.stride()[:3])
+    arr = (ctypes.c_int64 * len(vals))(*vals)
+    return arr, [ctypes.byref(arr, 24 * i) for i in range(len(ts))]
+
+
+try:
+    _raw_stream = torch._C._cuda_getCurrentRawStream   # the current stream's hipStream_t as an int
+except AttributeError:   # pragma: no cover - older torch
+    def _raw_stream(index):
+        return torch.cuda.current_stream(index).cuda_stream
+
+
+def _run(dev: torch.device, fn, *args):
+    """Call fn(*args) with dev as the current device (switching only if needed)."""
+    if dev.index == torch.cuda.current_device():
+        return fn(*args)
+    with torch.cuda.device(dev):
+        return fn(*args)
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
 def _stream(dev: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    return _raw_stream(dev.index)
 
 
 def _usable(t: torch.Tensor) -> torch.Tensor:
@@ -152,12 +177,13 @@ def forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, softmax_scale: fl
     if tuple(V.shape) != (B, Hkv, Nk, d):
         raise RuntimeError("V shape mismatch")
     Q, K, V = _usable(Q), _usable(K), _usable(V)
-    O = torch.empty((B, Hq, N, d), dtype=torch.float16, device=Q.device)
-    L = torch.empty((B, Hq, N), dtype=torch.float32, device=Q.device)
-    with torch.cuda.device(Q.device):
-        _check(_lib.fal_fwd(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), B, Hq, Hkv, N, Nk, d,
-                            _strides(Q), _strides(K), _strides(V), _strides(O),
-                            float(softmax_scale), int(bool(is_causal)), _stream(Q.device)))
+    dev = Q.device
+    O = torch.empty((B, Hq, N, d), dtype=torch.float16, device=dev)
+    L = torch.empty((B, Hq, N), dtype=torch.float32, device=dev)
+    arr, (qs, ks, vs, os_) = _stride_block(Q, K, V, O)
+    _check(_run(dev, lambda: _lib.fal_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), L.data_ptr(),
+                                          B, Hq, Hkv, N, Nk, d, qs, ks, vs, os_, float(softmax_scale),
+                                          int(bool(is_causal)), _raw_stream(dev.index))))
     return [O, L]
 
 
