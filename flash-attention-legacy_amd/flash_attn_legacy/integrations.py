@@ -46,11 +46,34 @@ def _mask_to_bias(attention_mask: torch.Tensor, batch: int, kv_len: int):
     return row.float()
 
 
+def _padded_prefill(query, key, value, keep, scaling, is_causal):
+    """Prefill of a padded batch: the tokens that ``keep`` [B, N] (bool, True = real
+    token) marks are packed into one varlen batch, attended with the varlen kernel
+    (causal within each sequence's own tokens), and scattered back; padded query rows
+    are zero.  This is what FlashAttention-2's HF path computes for a 2-D padding mask."""
+    from .flash_attn import flash_attn_varlen_func
+    B, H_q, N, d = query.shape
+    H_kv = key.shape[1]
+    flat = keep.reshape(-1)
+    idx = flat.nonzero().squeeze(1)
+    seqlens = keep.sum(1, dtype=torch.int32)
+    cu = torch.nn.functional.pad(torch.cumsum(seqlens, 0, dtype=torch.int32), (1, 0))
+    max_len = int(seqlens.max())
+    pack = lambda t, h: t.transpose(1, 2).reshape(B * N, h, d).index_select(0, idx)
+    o = flash_attn_varlen_func(pack(query, H_q), pack(key, H_kv), pack(value, H_kv), cu, cu, max_len, max_len,
+                               softmax_scale=scaling, causal=is_causal)
+    out = o.new_zeros((B * N, H_q, d)).index_copy(0, idx, o)
+    return out.view(B, N, H_q, d).transpose(1, 2)
+
+
 def _eager(query, key, value, attention_mask, scaling, is_causal):
     """The reference's eager branch (integrations.py:80-98), used only for inputs outside
     the kernels' contract (unsupported head_dim, per-head masks, masked multi-token
-    queries against a longer cache)."""
+    queries against a longer cache).  A 2-D padding mask [B, kv] (True or 1 = keep)
+    applies to every query row."""
     q_len, kv_len = query.shape[2], key.shape[2]
+    if attention_mask is not None and attention_mask.dim() == 2:
+        attention_mask = attention_mask[:, None, None, -kv_len:].bool()
     H_q, H_kv = query.shape[1], key.shape[1]
     if H_kv != H_q:
         rep = H_q // H_kv
@@ -83,8 +106,10 @@ def flash_attn_legacy_forward(
 ):
     """Attention function for transformers' AttentionInterface (reference integrations.py:24-103).
 
-    * prefill (q_len == kv_len): flash kernel; like the reference, ``attention_mask``
-      is not applied on this branch (causality comes from ``is_causal``);
+    * prefill (q_len == kv_len): flash kernel.  A 2-D padding mask (what transformers
+      passes for this implementation, once ``register`` has given it FlashAttention-2's
+      mask function) takes the varlen kernel over the unpadded tokens; a 4-D mask is
+      not applied, as in the reference (causality comes from ``is_causal``);
     * decode (q_len == 1 < kv_len): split-K decode kernel over the [B, H_kv, S, d]
       cache, with the mask's last row as an additive bias;
     * q_len != kv_len > 1 without a mask: forward kernel with top-left causal
@@ -116,7 +141,14 @@ def flash_attn_legacy_forward(
     half = lambda t: t.half() if t.dtype != torch.float16 else t
     attn_output = None
 
-    if d in _HEAD_DIMS and q_len == kv_len:
+    if d in _HEAD_DIMS and q_len == kv_len and attention_mask is not None and attention_mask.dim() == 2:
+        keep = attention_mask[:, -kv_len:].bool()
+        if bool(keep.all()):
+            attn_output = flash_attention(half(query), half(key), half(value),
+                                          softmax_scale=scaling, is_causal=is_causal)
+        else:
+            attn_output = _padded_prefill(half(query), half(key), half(value), keep, scaling, is_causal)
+    elif d in _HEAD_DIMS and q_len == kv_len:
         attn_output = flash_attention(half(query), half(key), half(value),
                                       softmax_scale=scaling, is_causal=is_causal)
     elif d in _HEAD_DIMS and q_len == 1 and H_q // key.shape[1] <= 32:
@@ -157,7 +189,10 @@ def register():
     """Register flash_attn_legacy in transformers' attention registry (reference
     integrations.py:106-161).
 
-    1. ``ALL_ATTENTION_FUNCTIONS.register("flash_attn_legacy", flash_attn_legacy_forward)``.
+    1. ``ALL_ATTENTION_FUNCTIONS.register("flash_attn_legacy", flash_attn_legacy_forward)``,
+       and FlashAttention-2's mask function for the same name, so that padded batches
+       arrive with their 2-D padding mask (without it transformers passes no mask at
+       all to an implementation it does not know, and padding is silently attended).
     2. Wrap ``PreTrainedModel._check_and_adjust_attn_implementation`` so this name skips
        transformers' flash-attention preload (any name containing "flash" triggers it),
        and falls back to "sdpa" for head dims the kernels do not support.
@@ -168,6 +203,11 @@ def register():
         from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS, PreTrainedModel
 
         ALL_ATTENTION_FUNCTIONS.register("flash_attn_legacy", flash_attn_legacy_forward)
+        try:
+            from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, flash_attention_mask
+            ALL_MASK_ATTENTION_FUNCTIONS.register("flash_attn_legacy", flash_attention_mask)
+        except ImportError:   # older transformers build 4-D masks for every implementation
+            pass
 
         original_check = PreTrainedModel._check_and_adjust_attn_implementation
         if getattr(original_check, "_flash_attn_legacy_patch", False):

@@ -57,6 +57,9 @@ def test_hf_registration():
     assert flash_attn_legacy.register() is True
     assert ALL_ATTENTION_FUNCTIONS["flash_attn_legacy"] is flash_attn_legacy_forward
     assert getattr(PreTrainedModel._check_and_adjust_attn_implementation, "_flash_attn_legacy_patch", False)
+    # padded batches reach the attention function with their 2-D padding mask
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, flash_attention_mask
+    assert ALL_MASK_ATTENTION_FUNCTIONS["flash_attn_legacy"] is flash_attention_mask
     # idempotent: registering again does not wrap the check twice
     flash_attn_legacy.register()
     chk = PreTrainedModel._check_and_adjust_attn_implementation
@@ -85,6 +88,23 @@ def test_mask_reduction_for_decode():
     b = _mask_to_bias(pad, 2, 3)
     assert torch.isneginf(b[0, 2]) and (b[1] == 0).all()
     assert _mask_to_bias(torch.zeros(2, 4, 1, 5), 2, 5) is None    # per-head mask: not reducible
+
+
+def test_eager_fallback_takes_2d_padding_mask():
+    """A 2-D padding mask in the eager branch equals the same mask as an additive 4-D
+    row broadcast over heads and query rows (and keys it masks get zero weight)."""
+    from flash_attn_legacy.integrations import _eager
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 3, 8, generator=g) for _ in range(3))
+    pad = torch.tensor([[0, 1, 1, 1, 1], [1, 1, 1, 1, 1]])
+    k5, v5 = torch.randn(2, 4, 5, 8, generator=g), torch.randn(2, 4, 5, 8, generator=g)
+    add = torch.zeros(2, 1, 1, 5).masked_fill(pad[:, None, None, :] == 0, float("-inf"))
+    a = _eager(q, k5, v5, pad, 0.3, False)
+    b = _eager(q, k5, v5, add, 0.3, False)
+    assert torch.allclose(a, b)
+    v5b = v5.clone()
+    v5b[0, :, 0] += 100.0           # the padded key's value must not matter
+    assert torch.allclose(_eager(q, k5, v5b, pad, 0.3, False), a)
 
 
 def test_utils_without_gpu():

@@ -120,3 +120,113 @@ def test_llama_monkey_patch_example(models):
         lb = eager(nxt, past_key_values=pb.past_key_values, use_cache=True).logits
     assert cos(la, lb) > 0.9999
     assert (la.float() - lb.float()).abs().max().item() < 0.05
+
+
+def padded_batch(seed):
+    """Two left-padded prompts of 80 tokens (30 and 0 pad tokens) and their mask."""
+    g = torch.Generator("cuda").manual_seed(seed)
+    ids = torch.randint(0, 256, (2, 80), device="cuda", generator=g)
+    mask = torch.ones_like(ids)
+    mask[0, :30] = 0
+    return ids, mask
+
+
+def test_padded_prefill_matches_eager(models):
+    """A padded batch: transformers passes this implementation the 2-D padding mask
+    (FlashAttention-2's mask function is registered for it), prefill runs the varlen
+    kernel over the real tokens, and the logits of real tokens match eager attention's."""
+    flash, eager = models
+    ids, mask = padded_batch(6)
+    with torch.no_grad():
+        a = flash(ids, attention_mask=mask).logits
+        b = eager(ids, attention_mask=mask).logits
+    real = mask.bool()
+    assert torch.isfinite(a[real]).all()
+    assert cos(a[real], b[real]) > 0.9999
+    assert (a[real].float() - b[real].float()).abs().max().item() < 0.05
+    # the padding changes the first sequence's result: it is not attended
+    with torch.no_grad():
+        c = flash(ids).logits
+    assert (a[0, -1].float() - c[0, -1].float()).abs().max().item() > 0.05
+
+
+def test_padded_cached_decode_matches_eager(models, monkeypatch):
+    """Decode step after a padded prefill: the mask's last row becomes the decode
+    kernel's additive bias."""
+    from flash_attn_legacy import hip_ext
+    flash, eager = models
+    calls = []
+    real = hip_ext.decode
+    monkeypatch.setattr(hip_ext, "decode", lambda *a, **k: calls.append(k.get("mask_bias")) or real(*a, **k))
+    ids, mask = padded_batch(7)
+    nxt = torch.randint(0, 256, (2, 1), device="cuda", generator=torch.Generator("cuda").manual_seed(8))
+    mask2 = torch.cat([mask, torch.ones_like(nxt)], dim=1)
+    with torch.no_grad():
+        pa = flash(ids, attention_mask=mask, use_cache=True)
+        la = flash(nxt, attention_mask=mask2, past_key_values=pa.past_key_values, use_cache=True).logits
+        pb = eager(ids, attention_mask=mask, use_cache=True)
+        lb = eager(nxt, attention_mask=mask2, past_key_values=pb.past_key_values, use_cache=True).logits
+    assert len(calls) == 2 and all(b is not None for b in calls)
+    assert cos(la, lb) > 0.9999
+    assert (la.float() - lb.float()).abs().max().item() < 0.05
+
+
+def test_padded_backward_matches_eager():
+    flash = tiny_llama("flash_attn_legacy")
+    eager = tiny_llama("eager")
+    eager.load_state_dict(flash.state_dict())
+    ids, mask = padded_batch(9)
+    # causal-LM labels shift by one: the last padded position (29) would predict the
+    # first real token; its output is padding's (zeros here, eager attention's
+    # uniform average there), so that label is masked too
+    labels = ids.masked_fill(mask == 0, -100)
+    labels[0, 30] = -100
+    la = flash(ids, attention_mask=mask, labels=labels).loss
+    lb = eager(ids, attention_mask=mask, labels=labels).loss
+    assert abs(la.item() - lb.item()) < 1e-2
+    la.backward()
+    lb.backward()
+    pa = dict(flash.named_parameters())
+    for name, p in eager.named_parameters():
+        if p.grad is not None and "self_attn" in name:
+            assert cos(pa[name].grad, p.grad) > 0.999, name
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_padded_prefill_attention_against_fp32(causal):
+    """The integration's padded-prefill branch on its own: output and q/k/v gradients
+    of the real rows against fp32 attention with the padding mask (keys masked out,
+    causal over positions), GQA 8/2, head_dim 64."""
+    import math
+    from flash_attn_legacy.integrations import flash_attn_legacy_forward
+    g = torch.Generator().manual_seed(10)
+    B, Hq, Hk, N, d = 3, 8, 2, 72, 64
+    q = torch.randn(B, Hq, N, d, generator=g).half().cuda().requires_grad_(True)
+    k = torch.randn(B, Hk, N, d, generator=g).half().cuda().requires_grad_(True)
+    v = torch.randn(B, Hk, N, d, generator=g).half().cuda().requires_grad_(True)
+    keep = torch.ones(B, N, dtype=torch.bool)
+    keep[0, :20] = False            # left padding
+    keep[2, 50:] = False            # right padding
+    mod = type("M", (), {"is_causal": causal})()
+    o, _ = flash_attn_legacy_forward(mod, q, k, v, keep.cuda(), scaling=1 / math.sqrt(d))
+    do = torch.randn(B, N, Hq, d, generator=g).half().cuda()
+    o.backward(do)
+
+    qf, kf, vf = (t.detach().float().cpu().requires_grad_(True) for t in (q, k, v))
+    kr, vr = kf.repeat_interleave(Hq // Hk, 1), vf.repeat_interleave(Hq // Hk, 1)
+    s = qf @ kr.transpose(-1, -2) / math.sqrt(d)
+    allowed = keep[:, None, None, :].expand(B, 1, N, N)
+    if causal:
+        allowed = allowed & torch.ones(N, N, dtype=torch.bool).tril()
+    # fully masked (padded) query rows get finite uniform weights; they carry no gradient
+    p = torch.softmax(s.masked_fill(~allowed, -1e9), -1)
+    ref = (p @ vr).transpose(1, 2)                      # [B, N, H, d]
+    real = keep
+    ref[real].backward(do.float().cpu()[real])
+    out = o.detach().float().cpu()
+    assert (out[real] - ref[real].detach()).abs().max().item() < 2e-3
+    assert (out[~real] == 0).all()
+    for name, a, r in (("dq", q.grad, qf.grad), ("dk", k.grad, kf.grad), ("dv", v.grad, vf.grad)):
+        a = a.float().cpu()
+        err = ((a - r).norm() / r.norm()).item()
+        assert err < 1e-2, (name, err)
