@@ -95,10 +95,10 @@ int fal_device_supported(int device) {
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
+static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
             int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream) {
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream, int bf16) {
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
   if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(seqlen_q) || !dims_ok(seqlen_k))
@@ -114,6 +114,7 @@ int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, in
   if (batch == 0 || seqlen_q == 0) return ok();
 
   FwdParams p{};
+  p.bf16 = bf16;
   p.q = static_cast<const half_t*>(q);
   p.k = static_cast<const half_t*>(k);
   p.v = static_cast<const half_t*>(v);
@@ -135,6 +136,20 @@ int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, in
                                   static_cast<hipStream_t>(stream)),
                        "fal_fwd");
 }
+int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
+            int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
+            const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream) {
+  return fal_fwd_impl(q, k, v, o, lse, batch, heads_q, heads_kv, seqlen_q, seqlen_k, head_dim, q_strides,
+                      k_strides, v_strides, o_strides, softmax_scale, is_causal, stream, 0);
+}
+int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
+            int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
+            const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream) {
+  return fal_fwd_impl(q, k, v, o, lse, batch, heads_q, heads_kv, seqlen_q, seqlen_k, head_dim, q_strides,
+                      k_strides, v_strides, o_strides, softmax_scale, is_causal, stream, 1);
+}
 
 size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q, int64_t head_dim) {
   (void)max_seqlen_q;
@@ -143,12 +158,12 @@ size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
   return align256((size_t)cap * sizeof(int2));
 }
 
-int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* lse,
+static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void* o, float* lse,
                    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t total_q,
                    int64_t total_k, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_q,
                    int64_t max_seqlen_k, const int64_t* q_strides, const int64_t* k_strides,
                    const int64_t* v_strides, const int64_t* o_strides, float softmax_scale, int is_causal,
-                   void* workspace, size_t workspace_bytes, void* stream) {
+                   void* workspace, size_t workspace_bytes, void* stream, int bf16) {
   (void)max_seqlen_k;
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
@@ -180,6 +195,7 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
   if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
 
   FwdParams p{};
+  p.bf16 = bf16;
   p.q = static_cast<const half_t*>(q);
   p.k = static_cast<const half_t*>(k);
   p.v = static_cast<const half_t*>(v);
@@ -203,6 +219,26 @@ int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* 
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
   return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), st),
                        "fal_fwd_varlen");
+}
+int fal_fwd_varlen(const void* q, const void* k, const void* v, void* o, float* lse,
+                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t total_q,
+                   int64_t total_k, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_q,
+                   int64_t max_seqlen_k, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* o_strides, float softmax_scale, int is_causal,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  return fal_fwd_varlen_impl(q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, num_seqs, total_q, total_k, heads_q,
+                             heads_kv, head_dim, max_seqlen_q, max_seqlen_k, q_strides, k_strides, v_strides,
+                             o_strides, softmax_scale, is_causal, workspace, workspace_bytes, stream, 0);
+}
+int fal_fwd_varlen_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t total_q,
+                   int64_t total_k, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_q,
+                   int64_t max_seqlen_k, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* o_strides, float softmax_scale, int is_causal,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  return fal_fwd_varlen_impl(q, k, v, o, lse, cu_seqlens_q, cu_seqlens_k, num_seqs, total_q, total_k, heads_q,
+                             heads_kv, head_dim, max_seqlen_q, max_seqlen_k, q_strides, k_strides, v_strides,
+                             o_strides, softmax_scale, is_causal, workspace, workspace_bytes, stream, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -273,18 +309,19 @@ static int run_bwd(BwdParams& p, int d, int causal, dim3 grid, dim3 dq_grid, boo
   return launch_status(e, "bwd dq cast");
 }
 
-int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+static int fal_bwd_impl(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
             void* dq, void* dk, void* dv, int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t seqlen_q,
             int64_t seqlen_k, int64_t head_dim, const int64_t* do_strides, const int64_t* q_strides,
             const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
             const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
-            float softmax_scale, int is_causal, void* workspace, size_t workspace_bytes, void* stream) {
+            float softmax_scale, int is_causal, void* workspace, size_t workspace_bytes, void* stream, int bf16) {
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
   if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(seqlen_q) || !dims_ok(seqlen_k))
     return fail(FAL_ERR_INVALID, "invalid sizes");
   if (heads_q % heads_kv != 0) return fail(FAL_ERR_INVALID, "H_q must be divisible by H_kv for GQA");
   BwdParams p{};
+  p.bf16 = bf16;
   int rc = fill_bwd_common(p, dout, q, k, v, o, lse, dq, dk, dv, do_strides, q_strides, k_strides, v_strides,
                            o_strides, dq_strides, dk_strides, dv_strides, true);
   if (rc) return rc;
@@ -311,6 +348,28 @@ int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const
   return run_bwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), dim3((unsigned)dq_blocks), true,
                  static_cast<hipStream_t>(stream));
 }
+int fal_bwd(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+            void* dq, void* dk, void* dv, int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t seqlen_q,
+            int64_t seqlen_k, int64_t head_dim, const int64_t* do_strides, const int64_t* q_strides,
+            const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+            const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+            float softmax_scale, int is_causal, void* workspace, size_t workspace_bytes, void* stream) {
+  return fal_bwd_impl(dout, q, k, v, o, lse, dq, dk, dv, batch, heads_q, heads_kv, seqlen_q, seqlen_k,
+                      head_dim, do_strides, q_strides, k_strides, v_strides, o_strides, dq_strides,
+                      dk_strides, dv_strides, softmax_scale, is_causal, workspace, workspace_bytes, stream,
+                      0);
+}
+int fal_bwd_bf16(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+            void* dq, void* dk, void* dv, int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t seqlen_q,
+            int64_t seqlen_k, int64_t head_dim, const int64_t* do_strides, const int64_t* q_strides,
+            const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+            const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+            float softmax_scale, int is_causal, void* workspace, size_t workspace_bytes, void* stream) {
+  return fal_bwd_impl(dout, q, k, v, o, lse, dq, dk, dv, batch, heads_q, heads_kv, seqlen_q, seqlen_k,
+                      head_dim, do_strides, q_strides, k_strides, v_strides, o_strides, dq_strides,
+                      dk_strides, dv_strides, softmax_scale, is_causal, workspace, workspace_bytes, stream,
+                      1);
+}
 
 size_t fal_bwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q,
                                      int64_t head_dim) {
@@ -326,14 +385,14 @@ size_t fal_bwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
   return bytes;
 }
 
-int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
                    void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                    int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,
                    int64_t head_dim, int64_t max_seqlen_q, int64_t max_seqlen_k, const int64_t* do_strides,
                    const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
                    const int64_t* o_strides, const int64_t* dq_strides, const int64_t* dk_strides,
                    const int64_t* dv_strides, float softmax_scale, int is_causal, void* workspace,
-                   size_t workspace_bytes, void* stream) {
+                   size_t workspace_bytes, void* stream, int bf16) {
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
   if (num_seqs < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(total_q) || !dims_ok(total_k) ||
@@ -342,6 +401,7 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
   if (heads_q % heads_kv != 0) return fail(FAL_ERR_INVALID, "H_q must be divisible by H_kv for GQA");
   if (!cu_seqlens_q || !cu_seqlens_k) return fail(FAL_ERR_INVALID, "cu_seqlens: null pointer");
   BwdParams p{};
+  p.bf16 = bf16;
   int rc = fill_bwd_common(p, dout, q, k, v, o, lse, dq, dk, dv, do_strides, q_strides, k_strides, v_strides,
                            o_strides, dq_strides, dk_strides, dv_strides, false);
   if (rc) return rc;
@@ -397,6 +457,32 @@ int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v
   }
   return run_bwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_kv), dq_grid, false, st);
 }
+int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+                   void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                   int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,
+                   int64_t head_dim, int64_t max_seqlen_q, int64_t max_seqlen_k, const int64_t* do_strides,
+                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, const int64_t* dq_strides, const int64_t* dk_strides,
+                   const int64_t* dv_strides, float softmax_scale, int is_causal, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return fal_bwd_varlen_impl(dout, q, k, v, o, lse, dq, dk, dv, cu_seqlens_q, cu_seqlens_k, num_seqs, total_q,
+                             total_k, heads_q, heads_kv, head_dim, max_seqlen_q, max_seqlen_k, do_strides,
+                             q_strides, k_strides, v_strides, o_strides, dq_strides, dk_strides, dv_strides,
+                             softmax_scale, is_causal, workspace, workspace_bytes, stream, 0);
+}
+int fal_bwd_varlen_bf16(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
+                   void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                   int64_t num_seqs, int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,
+                   int64_t head_dim, int64_t max_seqlen_q, int64_t max_seqlen_k, const int64_t* do_strides,
+                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, const int64_t* dq_strides, const int64_t* dk_strides,
+                   const int64_t* dv_strides, float softmax_scale, int is_causal, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return fal_bwd_varlen_impl(dout, q, k, v, o, lse, dq, dk, dv, cu_seqlens_q, cu_seqlens_k, num_seqs, total_q,
+                             total_k, heads_q, heads_kv, head_dim, max_seqlen_q, max_seqlen_k, do_strides,
+                             q_strides, k_strides, v_strides, o_strides, dq_strides, dk_strides, dv_strides,
+                             softmax_scale, is_causal, workspace, workspace_bytes, stream, 1);
+}
 
 // ---------------------------------------------------------------------------
 // Decode
@@ -412,11 +498,11 @@ size_t fal_decode_workspace_size(int64_t batch, int64_t heads_q, int64_t heads_k
          align256((size_t)batch * ms * sizeof(int2));
 }
 
-int fal_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
+static int fal_decode_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
                const float* mask_bias, int64_t mask_stride, void* o, float* lse, int64_t batch, int64_t heads_q,
                int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_k, const int64_t* q_strides,
                const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
-               float softmax_scale, void* workspace, size_t workspace_bytes, void* stream) {
+               float softmax_scale, void* workspace, size_t workspace_bytes, void* stream, int bf16) {
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
   if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(max_seqlen_k))
@@ -435,6 +521,7 @@ int fal_decode(const void* q, const void* k_cache, const void* v_cache, const in
     return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
   if (batch == 0) return ok();
   DecodeParams p{};
+  p.bf16 = bf16;
   p.q = static_cast<const half_t*>(q);
   p.k = static_cast<const half_t*>(k_cache);
   p.v = static_cast<const half_t*>(v_cache);
@@ -461,6 +548,24 @@ int fal_decode(const void* q, const void* k_cache, const void* v_cache, const in
   if ((int64_t)batch * p.max_splits * heads_kv * ((heads_q / heads_kv + 15) / 16) > 0x7fffffff)
     return fail(FAL_ERR_INVALID, "batch too large for one launch");
   return launch_status(launch_decode(p, (int)head_dim, static_cast<hipStream_t>(stream)), "fal_decode");
+}
+int fal_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
+               const float* mask_bias, int64_t mask_stride, void* o, float* lse, int64_t batch, int64_t heads_q,
+               int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_k, const int64_t* q_strides,
+               const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+               float softmax_scale, void* workspace, size_t workspace_bytes, void* stream) {
+  return fal_decode_impl(q, k_cache, v_cache, cache_seqlens, mask_bias, mask_stride, o, lse, batch, heads_q,
+                         heads_kv, head_dim, max_seqlen_k, q_strides, k_strides, v_strides, o_strides,
+                         softmax_scale, workspace, workspace_bytes, stream, 0);
+}
+int fal_decode_bf16(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
+               const float* mask_bias, int64_t mask_stride, void* o, float* lse, int64_t batch, int64_t heads_q,
+               int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_k, const int64_t* q_strides,
+               const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+               float softmax_scale, void* workspace, size_t workspace_bytes, void* stream) {
+  return fal_decode_impl(q, k_cache, v_cache, cache_seqlens, mask_bias, mask_stride, o, lse, batch, heads_q,
+                         heads_kv, head_dim, max_seqlen_k, q_strides, k_strides, v_strides, o_strides,
+                         softmax_scale, workspace, workspace_bytes, stream, 1);
 }
 
 }  // extern "C"

@@ -34,9 +34,11 @@ namespace fal {
 template <int D>
 constexpr int row_group() { return D / 8 <= 4 ? 4 : D / 8 <= 8 ? 8 : D / 8 <= 16 ? 16 : 32; }
 
-template <int D>
+template <class T, int D>
 __global__ void __launch_bounds__(256)
 bwd_pre_kernel(BwdParams p, int rows, int batched) {
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
   constexpr int G = row_group<D>();   // lanes per row (power of two; lanes past D idle)
   const int r = blockIdx.x * (256 / G) + threadIdx.x / G;
   const int c = (threadIdx.x % G) * 8;
@@ -60,8 +62,8 @@ bwd_pre_kernel(BwdParams p, int rows, int batched) {
   }
   float s = 0.f;
   if (c < D) {
-    const half8 a = load_h8(p.o + o_off + c);
-    const half8 g = load_h8(p.dout + do_off + c);
+    const V8 a = ld8((const T*)p.o + o_off + c);
+    const V8 g = ld8((const T*)p.dout + do_off + c);
 #pragma unroll
     for (int j = 0; j < 8; ++j) s = fmaf((float)a[j], (float)g[j], s);
   }
@@ -75,9 +77,11 @@ bwd_pre_kernel(BwdParams p, int rows, int batched) {
 }
 
 // dQ = fp16(dq_acc * scale)
-template <int D>
+template <class T, int D>
 __global__ void __launch_bounds__(256)
 bwd_post_kernel(BwdParams p, int rows, int batched) {
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
   constexpr int G = row_group<D>();
   const int r = blockIdx.x * (256 / G) + threadIdx.x / G;
   const int c = (threadIdx.x % G) * 8;
@@ -97,21 +101,23 @@ bwd_post_kernel(BwdParams p, int rows, int batched) {
   }
   const f32x4 x0 = *reinterpret_cast<const f32x4*>(p.dq_acc + qa_off + c);
   const f32x4 x1 = *reinterpret_cast<const f32x4*>(p.dq_acc + qa_off + c + 4);
-  half8 h;
+  V8 h;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    h[j] = (half_t)(x0[j] * p.scale);
-    h[j + 4] = (half_t)(x1[j] * p.scale);
+    h[j] = (T)(x0[j] * p.scale);
+    h[j + 4] = (T)(x1[j] * p.scale);
   }
-  store_u4(p.dq + dq_off + c, __builtin_bit_cast(u32x4, h));
+  st_u4((T*)p.dq + dq_off + c, __builtin_bit_cast(u32x4, h));
 }
 
 // --------------------------------------------------------------------------
 // Main KV-outer kernel
 // --------------------------------------------------------------------------
-template <int D, int NW, int BMQ, bool CAUSAL>
+template <class T, int D, int NW, int BMQ, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64)
 bwd_kernel(BwdParams p) {
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
   static_assert(BMQ == 32, "query tile is one 32-row MFMA block");
   constexpr int BN = NW * 32;
   constexpr int KS = D / 16;
@@ -125,10 +131,10 @@ bwd_kernel(BwdParams p) {
   constexpr int QCPT = (QCH + NW * 64 - 1) / (NW * 64);
   constexpr int CPR = D / 8;
 
-  __shared__ __attribute__((aligned(16))) half_t ks_s[BN * LDK];
-  __shared__ __attribute__((aligned(16))) half_t q_s[BMQ * LDK];
-  __shared__ __attribute__((aligned(16))) half_t do_s[BMQ * LDK];
-  __shared__ __attribute__((aligned(16))) half_t dst_s[BN * LDQ];
+  __shared__ __attribute__((aligned(16))) T ks_s[BN * LDK];
+  __shared__ __attribute__((aligned(16))) T q_s[BMQ * LDK];
+  __shared__ __attribute__((aligned(16))) T do_s[BMQ * LDK];
+  __shared__ __attribute__((aligned(16))) T dst_s[BN * LDQ];
   __shared__ __attribute__((aligned(16))) float l_s[BMQ];
   __shared__ __attribute__((aligned(16))) float d_s[BMQ];
 
@@ -165,23 +171,23 @@ bwd_kernel(BwdParams p) {
   const int G = p.Hq / p.Hkv;
   const float c = p.scale_log2;
 
-  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
-  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
+  const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
+  const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
 
   // K/V rows of this wave (B operands: n = key, k = head dim)
   const int kw0 = n0 + w * 32;
   const int key = kw0 + l32;
-  half8 kreg[KS], vreg[KS];
+  V8 kreg[KS], vreg[KS];
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    kreg[t] = key < nk ? load_h8(kbase + (int64_t)key * p.k_ss + t * 16 + hh * 8) : zero_h8();
-    vreg[t] = key < nk ? load_h8(vbase + (int64_t)key * p.v_ss + t * 16 + hh * 8) : zero_h8();
+    kreg[t] = key < nk ? ld8(kbase + (int64_t)key * p.k_ss + t * 16 + hh * 8) : zero8<T>();
+    vreg[t] = key < nk ? ld8(vbase + (int64_t)key * p.v_ss + t * 16 + hh * 8) : zero8<T>();
   }
   // K tile, row-major, for dQ = dS K
   for (int ch = tid; ch < BN * CPR; ch += NW * 64) {
     const int r = ch / CPR, cc = (ch % CPR) * 8;
-    const u32x4 x = (n0 + r < nk) ? load_u4(kbase + (int64_t)(n0 + r) * p.k_ss + cc) : u32x4{0, 0, 0, 0};
-    store_u4(ks_s + r * LDK + cc, x);
+    const u32x4 x = (n0 + r < nk) ? ld_u4(kbase + (int64_t)(n0 + r) * p.k_ss + cc) : u32x4{0, 0, 0, 0};
+    st_u4(ks_s + r * LDK + cc, x);
   }
 
   const int nqt = cdiv(nq, BMQ);
@@ -200,8 +206,8 @@ bwd_kernel(BwdParams p) {
 
     for (int g = 0; g < G; ++g) {
       const int hq = hkv * G + g;
-      const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
-      const half_t* dobase = p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
+      const T* qbase = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
+      const T* dobase = (const T*)p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
       const float* lbase = p.lse + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
       const float* dbase_p = p.delta + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
       float* qabase = p.dq_acc + (int64_t)b * p.dqa_sb + (int64_t)hq * p.dqa_sh + (int64_t)q_off * p.dqa_ss;
@@ -215,8 +221,8 @@ bwd_kernel(BwdParams p) {
           const int ch = tid + i * NW * 64;
           const int r = ch / CPR, cc = (ch % CPR) * 8;
           const bool ok = (QCH % (NW * 64) == 0 || ch < QCH) && (q0 + r < nq);
-          qpre[i] = ok ? load_u4(qbase + (int64_t)(q0 + r) * p.q_ss + cc) : u32x4{0, 0, 0, 0};
-          dopre[i] = ok ? load_u4(dobase + (int64_t)(q0 + r) * p.do_ss + cc) : u32x4{0, 0, 0, 0};
+          qpre[i] = ok ? ld_u4(qbase + (int64_t)(q0 + r) * p.q_ss + cc) : u32x4{0, 0, 0, 0};
+          dopre[i] = ok ? ld_u4(dobase + (int64_t)(q0 + r) * p.do_ss + cc) : u32x4{0, 0, 0, 0};
         }
         if (tid < BMQ) {
           const int r = q0 + tid;
@@ -236,8 +242,8 @@ bwd_kernel(BwdParams p) {
           const int ch = tid + i * NW * 64;
           if (QCH % (NW * 64) == 0 || ch < QCH) {
             const int r = ch / CPR, cc = (ch % CPR) * 8;
-            store_u4(q_s + r * LDK + cc, qpre[i]);
-            store_u4(do_s + r * LDK + cc, dopre[i]);
+            st_u4(q_s + r * LDK + cc, qpre[i]);
+            st_u4(do_s + r * LDK + cc, dopre[i]);
           }
         }
         if (tid < BMQ) {
@@ -261,8 +267,8 @@ bwd_kernel(BwdParams p) {
           f32x16 s = zero_f16(), dp = zero_f16();
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            s = mfma32(load_h8(q_s + l32 * LDK + t * 16 + hh * 8), kreg[t], s);
-            dp = mfma32(load_h8(do_s + l32 * LDK + t * 16 + hh * 8), vreg[t], dp);
+            s = mfma32(ld8(q_s + l32 * LDK + t * 16 + hh * 8), kreg[t], s);
+            dp = mfma32(ld8(do_s + l32 * LDK + t * 16 + hh * 8), vreg[t], dp);
           }
           // P and dS (element i: query q0 + (i/4)*8 + hh*4 + i%4, key `key`)
 #pragma unroll
@@ -282,23 +288,23 @@ bwd_kernel(BwdParams p) {
           // dV^T += dO^T P ; dK^T += Q^T dS  (this pass's head-dim columns)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
-            const half8 pb = cvt8(s, ks);
-            const half8 sb = cvt8(dp, ks);
+            const V8 pb = cvt8t<T>(s, ks);
+            const V8 sb = cvt8t<T>(dp, ks);
 #pragma unroll
             for (int db = 0; db < DWB; ++db) {
               const int col = dbase + db * 32;
-              dv_acc[db] = mfma32(lds_kslab_tr(do_s + tofs_q + col, ks * 16, hh, LDK), pb, dv_acc[db]);
-              dk_acc[db] = mfma32(lds_kslab_tr(q_s + tofs_q + col, ks * 16, hh, LDK), sb, dk_acc[db]);
+              dv_acc[db] = mfma32(kslab_tr(do_s + tofs_q + col, ks * 16, hh, LDK), pb, dv_acc[db]);
+              dk_acc[db] = mfma32(kslab_tr(q_s + tofs_q + col, ks * 16, hh, LDK), sb, dk_acc[db]);
             }
           }
           if (pass == 0) {
             // dS^T (fp16) into LDS: row = key (local), columns = query rows
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-              half4 h;
+              V4 h;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) h[e] = (half_t)dp[g4 * 4 + e];
-              *reinterpret_cast<half4*>(dst_s + (w * 32 + l32) * LDQ + g4 * 8 + hh * 4) = h;
+              for (int e = 0; e < 4; ++e) h[e] = (T)dp[g4 * 4 + e];
+              *reinterpret_cast<V4*>(dst_s + (w * 32 + l32) * LDQ + g4 * 8 + hh * 4) = h;
             }
           }
         }
@@ -311,8 +317,8 @@ bwd_kernel(BwdParams p) {
             for (int ks = 0; ks < BN / 16; ++ks) {
               const int kwave0 = n0 + (ks >> 1) * 32;   // first key of the owning wave
               if (CAUSAL && q0 + BMQ - 1 < kwave0) break;
-              acc = mfma32(lds_kslab_tr(dst_s + tofs_s, ks * 16, hh, LDQ),
-                           lds_kslab_tr(ks_s + tofs_q + db * 32, ks * 16, hh, LDK), acc);
+              acc = mfma32(kslab_tr(dst_s + tofs_s, ks * 16, hh, LDQ),
+                           kslab_tr(ks_s + tofs_q + db * 32, ks * 16, hh, LDK), acc);
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -329,21 +335,21 @@ bwd_kernel(BwdParams p) {
 
     // write dK (scaled) and dV for this pass's columns
     if (key < nk) {
-      half_t* dkrow = p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + (int64_t)(k_off + key) * p.dk_ss;
-      half_t* dvrow = p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + (int64_t)(k_off + key) * p.dv_ss;
+      T* dkrow = (T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + (int64_t)(k_off + key) * p.dk_ss;
+      T* dvrow = (T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + (int64_t)(k_off + key) * p.dv_ss;
 #pragma unroll
       for (int db = 0; db < DWB; ++db)
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          half4 hk, hv;
+          V4 hk, hv;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            hk[e] = (half_t)(dk_acc[db][g4 * 4 + e] * p.scale);
-            hv[e] = (half_t)dv_acc[db][g4 * 4 + e];
+            hk[e] = (T)(dk_acc[db][g4 * 4 + e] * p.scale);
+            hv[e] = (T)dv_acc[db][g4 * 4 + e];
           }
           const int col = dbase + db * 32 + g4 * 8 + hh * 4;
-          *reinterpret_cast<half4*>(dkrow + col) = hk;
-          *reinterpret_cast<half4*>(dvrow + col) = hv;
+          *reinterpret_cast<V4*>(dkrow + col) = hk;
+          *reinterpret_cast<V4*>(dvrow + col) = hv;
         }
     }
   }
@@ -386,9 +392,15 @@ bwd_kernel(BwdParams p) {
 #ifndef FAL_BWD2_NW
 #define FAL_BWD2_NW 4   // waves per workgroup: 4 (64 keys, 2 workgroups per CU) or 8 (128 keys, double-buffered Q/dO)
 #endif
-template <int D, bool CAUSAL>
+template <class T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(FAL_BWD2_NW * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
 bwd2_kernel(BwdParams p) {
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
+  // fp16: the K tile is pre-multiplied by scale*log2(e) in LDS and the S accumulator
+  // starts at -L*log2e; bf16 keeps K exact (8-bit mantissa) and applies both to the
+  // fp32 scores with one FMA each
+  constexpr bool PRESCALE = std::is_same<T, half_t>::value;
   using TL = SwizzledTile<D>;
   constexpr int NW = FAL_BWD2_NW, BN = NW * 16, BMQ = 64;
   constexpr int NKG = NW / 2;             // key groups of 32 (x 2 query halves)
@@ -403,9 +415,9 @@ bwd2_kernel(BwdParams p) {
   static_assert(BMQ * CPR % (NW * 64) == 0, "Q tile must split evenly over the waves");
   static_assert((DBUF ? 2 : 1) * 2 * QPART * 2 >= NKG * 32 * D * 4, "dK/dV reduction reuses the Q/dO buffers");
 
-  __shared__ __attribute__((aligned(1024))) half_t ks_s[KPART];
-  __shared__ __attribute__((aligned(1024))) half_t vs_s[KPART];
-  __shared__ __attribute__((aligned(1024))) half_t qd_s[(DBUF ? 2 : 1) * 2 * QPART];   // [buffer][Q, dO]
+  __shared__ __attribute__((aligned(1024))) T ks_s[KPART];
+  __shared__ __attribute__((aligned(1024))) T vs_s[KPART];
+  __shared__ __attribute__((aligned(1024))) T qd_s[(DBUF ? 2 : 1) * 2 * QPART];   // [buffer][Q, dO]
   __shared__ float l_s[2][BMQ];
   __shared__ float d_s[2][BMQ];
 
@@ -447,8 +459,8 @@ bwd2_kernel(BwdParams p) {
   }
   const int G = p.Hq / p.Hkv;
   const float c = p.scale_log2;
-  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
-  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
+  const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
+  const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
 
   // per-lane direct-load byte offsets from a tile's first row (instruction i of wave ws
   // fills chunks [(i*NW+ws)*64, +64)); one buffer resource per tile bounds the rows
@@ -484,10 +496,10 @@ bwd2_kernel(BwdParams p) {
     return POW2 ? (trb[hf] ^ ((db * 4) << 3)) : TL::offset(hf * 8 + trl, db * 4 + trc);
   };
   // 8 k-slots for rows row0.. (multiple of 16) of a swizzled D-column tile, block db
-  auto trk = [&](const half_t* base, int db, int row0) {
-    const half4 lo = lds_read_tr(base + tra(0, db) + tr_lo + row0 * CPR * 8);
-    const half4 hi = lds_read_tr(base + tra(1, db) + tr_lo + row0 * CPR * 8);
-    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  auto trk = [&](const T* base, int db, int row0) {
+    const V4 lo = lds_tr(base + tra(0, db) + tr_lo + row0 * CPR * 8);
+    const V4 hi = lds_tr(base + tra(1, db) + tr_lo + row0 * CPR * 8);
+    return join8(lo, hi);
   };
   const int nqt = cdiv(nq, BMQ);
 
@@ -525,12 +537,12 @@ bwd2_kernel(BwdParams p) {
     wait_vmcnt0();
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < KPART / (NW * 64 * 8); ++i) {
-      half_t* ptr = ks_s + (i * NW * 64 + tid) * 8;
-      half8 v = load_h8(ptr);
+    for (int i = 0; i < (PRESCALE ? KPART / (NW * 64 * 8) : 0); ++i) {
+      T* ptr = ks_s + (i * NW * 64 + tid) * 8;
+      V8 v = ld8(ptr);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] * c);
-      *reinterpret_cast<half8*>(ptr) = v;
+      for (int e = 0; e < 8; ++e) v[e] = (T)((float)v[e] * c);
+      *reinterpret_cast<V8*>(ptr) = v;
     }
     const int qt0 = CAUSAL ? (n0 / BMQ) : 0;
     // (query head, query tile) items of this key tile, in one sequence so the Q/dO
@@ -550,9 +562,9 @@ bwd2_kernel(BwdParams p) {
         f_qt = qt0;
         ++f_hq;
       }
-      const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)(q_off + q0) * p.q_ss;
-      const half_t* dobase =
-          p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)(q_off + q0) * p.do_ss;
+      const T* qbase = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)(q_off + q0) * p.q_ss;
+      const T* dobase =
+          (const T*)p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)(q_off + q0) * p.do_ss;
       const int64_t left = (int64_t)max(nq - q0, 0);
       const __amdgpu_buffer_rsrc_t qrs = make_rsrc(qbase, (uint32_t)min(left * p.q_ss * 2, (int64_t)0x7fffffff));
       const __amdgpu_buffer_rsrc_t dors = make_rsrc(dobase, (uint32_t)min(left * p.do_ss * 2, (int64_t)0x7fffffff));
@@ -591,8 +603,8 @@ bwd2_kernel(BwdParams p) {
         }
         __syncthreads();                  // barrier A: item in LDS; readers of item-1 done
         if (DBUF && item + 1 < nitems_q) fetch(buf ^ 1);
-        const half_t* q_s = qd_s + (buf * 2 + 0) * QPART + qh * 32 * CPR * 8;
-        const half_t* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
+        const T* q_s = qd_s + (buf * 2 + 0) * QPART + qh * 32 * CPR * 8;
+        const T* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
         const int qr0 = q0 + qh * 32;     // first query row of this wave's half
         if (!CAUSAL || qr0 + 31 >= kw0) {
           // S = Q K^T - L*log2e and dP = dO V^T - D
@@ -603,25 +615,25 @@ bwd2_kernel(BwdParams p) {
             const f32x4 dn = *reinterpret_cast<const f32x4*>(&d_s[buf][qh * 32 + g4 * 8 + hh * 4]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              s[g4 * 4 + e] = ln[e];
+              s[g4 * 4 + e] = PRESCALE ? ln[e] : 0.f;
               dp[g4 * 4 + e] = dn[e];
             }
           }
           __builtin_amdgcn_s_setprio(1);
           // operands of step t+1 are read before the MFMAs of step t
-          const half_t* kw_s = ks_s + kg * 32 * CPR * 8;
-          const half_t* vw_s = vs_s + kg * 32 * CPR * 8;
-          half8 oq = load_h8(q_s + faddr(0)), ok = load_h8(kw_s + faddr(0));
-          half8 od = load_h8(do_s + faddr(0)), ov = load_h8(vw_s + faddr(0));
+          const T* kw_s = ks_s + kg * 32 * CPR * 8;
+          const T* vw_s = vs_s + kg * 32 * CPR * 8;
+          V8 oq = ld8(q_s + faddr(0)), ok = ld8(kw_s + faddr(0));
+          V8 od = ld8(do_s + faddr(0)), ov = ld8(vw_s + faddr(0));
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            half8 nq, nk, nd, nv;
+            V8 nq, nk, nd, nv;
             if (t + 1 < KS) {
               const int fa = faddr(t + 1);
-              nq = load_h8(q_s + fa);
-              nk = load_h8(kw_s + fa);
-              nd = load_h8(do_s + fa);
-              nv = load_h8(vw_s + fa);
+              nq = ld8(q_s + fa);
+              nk = ld8(kw_s + fa);
+              nd = ld8(do_s + fa);
+              nv = ld8(vw_s + fa);
             }
             s = mfma32(oq, ok, s);
             dp = mfma32(od, ov, dp);
@@ -640,7 +652,13 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int i = g4 * 4 + e;
-                float pv = fast_exp2(s[i]);
+                float pv;
+                if (PRESCALE) {
+                  pv = fast_exp2(s[i]);
+                } else {
+                  const float ln = l_s[buf][qh * 32 + g4 * 8 + hh * 4 + e];
+                  pv = fast_exp2(fmaf(s[i], c, ln));
+                }
                 if (decltype(masked)::value && cthr > g4 * 8 + e) pv = 0.f;
                 s[i] = pv;
                 dp[i] = pv * dp[i];
@@ -653,17 +671,17 @@ bwd2_kernel(BwdParams p) {
           // dV^T += dO^T P ; dK^T += Q^T dS
           __builtin_amdgcn_s_setprio(1);
           {
-            half8 pb[2], sb[2];
+            V8 pb[2], sb[2];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-              pb[ks] = cvt8(s, ks);
-              sb[ks] = cvt8(dp, ks);
+              pb[ks] = cvt8t<T>(s, ks);
+              sb[ks] = cvt8t<T>(dp, ks);
             }
-            half8 ao = trk(do_s, 0, 0), aq = trk(q_s, 0, 0);
+            V8 ao = trk(do_s, 0, 0), aq = trk(q_s, 0, 0);
 #pragma unroll
             for (int st = 0; st < 2 * DWB; ++st) {
               const int ks = st / DWB, db = st % DWB;
-              half8 no, nq;
+              V8 no, nq;
               if (st + 1 < 2 * DWB) {
                 no = trk(do_s, (st + 1) % DWB, (st + 1) / DWB * 16);
                 nq = trk(q_s, (st + 1) % DWB, (st + 1) / DWB * 16);
@@ -689,7 +707,7 @@ bwd2_kernel(BwdParams p) {
     // query half stages its accumulators lane-contiguous, [kg][db][i][lane], and the
     // first adds them element by element (bank-conflict free, no transpose).
     float* red = reinterpret_cast<float*>(qd_s);
-    auto reduce_write = [&](f32x16 (&acc)[DWB], half_t* row, float sc) {
+    auto reduce_write = [&](f32x16 (&acc)[DWB], T* row, float sc) {
       float* mine = red + (size_t)kg * DWB * 16 * 64 + lane;
       if (qh == 1) {
 #pragma unroll
@@ -704,17 +722,17 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             const int col = db * 32 + g4 * 8 + hh * 4;
-            half4 h;
+            V4 h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)((acc[db][g4 * 4 + e] + mine[(db * 16 + g4 * 4 + e) * 64]) * sc);
-            *reinterpret_cast<half4*>(row + col) = h;
+            for (int e = 0; e < 4; ++e) h[e] = (T)((acc[db][g4 * 4 + e] + mine[(db * 16 + g4 * 4 + e) * 64]) * sc);
+            *reinterpret_cast<V4*>(row + col) = h;
           }
       }
       __syncthreads();
     };
     const int64_t krow = (int64_t)(k_off + min(key, max(nk - 1, 0)));
-    reduce_write(dk_acc, p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + krow * p.dk_ss, p.scale);
-    reduce_write(dv_acc, p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + krow * p.dv_ss, 1.f);
+    reduce_write(dk_acc, (T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + krow * p.dk_ss, p.scale);
+    reduce_write(dv_acc, (T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + krow * p.dv_ss, 1.f);
   }
 }
 
@@ -736,9 +754,11 @@ bwd2_kernel(BwdParams p) {
 #ifndef FAL_BWD_DQ_WPE
 #define FAL_BWD_DQ_WPE 2
 #endif
-template <int D, int NW, int BN, bool CAUSAL>
+template <class T, int D, int NW, int BN, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(FAL_BWD_DQ_WPE, 8)))
 bwd_dq_kernel(BwdParams p) {
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
   using TL = SwizzledTile<D>;
   constexpr int BM = NW * 32;
   constexpr int KS = D / 16;
@@ -749,7 +769,7 @@ bwd_dq_kernel(BwdParams p) {
   constexpr int IPT = BN * CPR / (NW * 64);
   static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(1024))) half_t smem[2 * 2 * PART];
+  __shared__ __attribute__((aligned(1024))) T smem[2 * 2 * PART];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -804,10 +824,10 @@ bwd_dq_kernel(BwdParams p) {
   const int m0 = qt * BM;
   if (m0 >= nq) continue;
 
-  const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
-  const half_t* dobase = p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
-  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
-  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
+  const T* qbase = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
+  const T* dobase = (const T*)p.dout + (int64_t)b * p.do_sb + (int64_t)hq * p.do_sh + (int64_t)q_off * p.do_ss;
+  const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
+  const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
   const int64_t lrow = (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
 
   // Q and dO slices of this wave (B operands: n = query row, k = head dim), the row's
@@ -815,25 +835,22 @@ bwd_dq_kernel(BwdParams p) {
   // half of the head dim each.  D is also stored for the dK/dV kernel, which runs after
   // this one.
   const int row = m0 + w * 32 + l32;
-  half8 qreg[KS], doreg[KS];
+  V8 qreg[KS], doreg[KS];
   float lrow2 = INFINITY, dpart = 0.f;
   if (row < nq) {
-    const half_t* orow = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)(q_off + row) * p.o_ss;
+    const T* orow = (const T*)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)(q_off + row) * p.o_ss;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
-      qreg[t] = load_h8(qbase + (int64_t)row * p.q_ss + t * 16 + hh * 8);
-      doreg[t] = load_h8(dobase + (int64_t)row * p.do_ss + t * 16 + hh * 8);
-      const half8 ov = load_h8(orow + t * 16 + hh * 8);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        dpart = __builtin_amdgcn_fdot2(half2v{doreg[t][2 * j], doreg[t][2 * j + 1]}, half2v{ov[2 * j], ov[2 * j + 1]},
-                                       dpart, false);
+      qreg[t] = ld8(qbase + (int64_t)row * p.q_ss + t * 16 + hh * 8);
+      doreg[t] = ld8(dobase + (int64_t)row * p.do_ss + t * 16 + hh * 8);
+      const V8 ov = ld8(orow + t * 16 + hh * 8);
+      dpart = dot8(doreg[t], ov, dpart);
     }
     const float L = p.lse[lrow + (int64_t)row * p.l_ss];
     lrow2 = (L == -INFINITY) ? INFINITY : L * kLog2e;
   } else {
 #pragma unroll
-    for (int t = 0; t < KS; ++t) qreg[t] = doreg[t] = zero_h8();
+    for (int t = 0; t < KS; ++t) qreg[t] = doreg[t] = zero8<T>();
   }
   const float drow = pair_sum(dpart);
   if (hh == 0 && row < nq) p.delta[lrow + (int64_t)row * p.l_ss] = drow;
@@ -870,8 +887,8 @@ bwd_dq_kernel(BwdParams p) {
 
   auto load_tile = [&](int tile, int buf) {
     const int n0 = tile * BN;
-    half_t* kdst = smem + buf * 2 * PART;
-    half_t* vdst = kdst + PART;
+    T* kdst = smem + buf * 2 * PART;
+    T* vdst = kdst + PART;
     const int64_t left = (int64_t)max(nk - n0, 0);
     const __amdgpu_buffer_rsrc_t krs =
         make_rsrc(kbase + (int64_t)n0 * p.k_ss, (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff));
@@ -892,25 +909,25 @@ bwd_dq_kernel(BwdParams p) {
   auto tile_body = [&](auto masked, int j, int buf) {
     constexpr bool MASK = decltype(masked)::value;
     const int n0 = j * BN;
-    const half_t* ks = smem + buf * 2 * PART;
-    const half_t* vs = ks + PART;
+    const T* ks = smem + buf * 2 * PART;
+    const T* vs = ks + PART;
     // S^T = K Q^T and dP^T = V dO^T; fragments read one k-step ahead of their MFMAs
     f32x16 sacc[NKB], pacc[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) sacc[kb] = pacc[kb] = zero_f16();
-    half8 kf[2][NKB], vf[2][NKB];
+    V8 kf[2][NKB], vf[2][NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      kf[0][kb] = load_h8(ks + kaddr[0] + kb * 32 * CPR * 8);
-      vf[0][kb] = load_h8(vs + kaddr[0] + kb * 32 * CPR * 8);
+      kf[0][kb] = ld8(ks + kaddr[0] + kb * 32 * CPR * 8);
+      vf[0][kb] = ld8(vs + kaddr[0] + kb * 32 * CPR * 8);
     }
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       if (t + 1 < KS) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-          kf[(t + 1) & 1][kb] = load_h8(ks + kaddr[t + 1] + kb * 32 * CPR * 8);
-          vf[(t + 1) & 1][kb] = load_h8(vs + kaddr[t + 1] + kb * 32 * CPR * 8);
+          kf[(t + 1) & 1][kb] = ld8(ks + kaddr[t + 1] + kb * 32 * CPR * 8);
+          vf[(t + 1) & 1][kb] = ld8(vs + kaddr[t + 1] + kb * 32 * CPR * 8);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * NKB, 0);
       }
@@ -938,13 +955,13 @@ bwd_dq_kernel(BwdParams p) {
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
-        const half8 sb = cvt8(pacc[kb], t2);
+        const V8 sb = cvt8t<T>(pacc[kb], t2);
         const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const half4 lo = lds_read_tr(ks + taddr[0][db] + kofs);
-          const half4 hi = lds_read_tr(ks + taddr[1][db] + kofs);
-          dqacc[db] = mfma32(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, sb, dqacc[db]);
+          const V4 lo = lds_tr(ks + taddr[0][db] + kofs);
+          const V4 hi = lds_tr(ks + taddr[1][db] + kofs);
+          dqacc[db] = mfma32(join8(lo, hi), sb, dqacc[db]);
         }
       }
   };
@@ -974,15 +991,15 @@ bwd_dq_kernel(BwdParams p) {
   }
 
   if (row < nq) {
-    half_t* dqrow = p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)(q_off + row) * p.dq_ss;
+    T* dqrow = (T*)p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)(q_off + row) * p.dq_ss;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        half4 h;
+        V4 h;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (half_t)(dqacc[db][g4 * 4 + e] * p.scale);
-        *reinterpret_cast<half4*>(dqrow + db * 32 + g4 * 8 + hh * 4) = h;
+        for (int e = 0; e < 4; ++e) h[e] = (T)(dqacc[db][g4 * 4 + e] * p.scale);
+        *reinterpret_cast<V4*>(dqrow + db * 32 + g4 * 8 + hh * 4) = h;
       }
   }
   }
@@ -1001,22 +1018,26 @@ int bwd_block_n(int d) {
   return split_d(d) ? FAL_BWD2_NW * 16 : kBwdNW * 32;
 }
 
-template <int D>
-static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+template <class T, int D>
+static hipError_t launch_bwd_t(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
   if constexpr (split_d(D)) {
     // batched causal: one workgroup per pair of key tiles
     if (!p.cu_q && causal) grid.x = (unsigned)((p.n_ktiles + 1) / 2) * p.B * p.Hkv;
     if (causal)
-      hipLaunchKernelGGL((bwd2_kernel<D, true>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
+      hipLaunchKernelGGL((bwd2_kernel<T, D, true>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
     else
-      hipLaunchKernelGGL((bwd2_kernel<D, false>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
+      hipLaunchKernelGGL((bwd2_kernel<T, D, false>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
   } else {
     if (causal)
-      hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, true>), grid, dim3(kBwdNW * 64), 0, st, p);
+      hipLaunchKernelGGL((bwd_kernel<T, D, kBwdNW, 32, true>), grid, dim3(kBwdNW * 64), 0, st, p);
     else
-      hipLaunchKernelGGL((bwd_kernel<D, kBwdNW, 32, false>), grid, dim3(kBwdNW * 64), 0, st, p);
+      hipLaunchKernelGGL((bwd_kernel<T, D, kBwdNW, 32, false>), grid, dim3(kBwdNW * 64), 0, st, p);
   }
   return hipGetLastError();
+}
+template <int D>
+static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+  return p.bf16 ? launch_bwd_t<bf16_t, D>(p, causal, grid, st) : launch_bwd_t<half_t, D>(p, causal, grid, st);
 }
 
 #ifndef FAL_BWD_DQ_BN
@@ -1030,15 +1051,20 @@ int bwd_dq_block_m(int d) {
   return kDqNW * 32;
 }
 
-template <int D>
-static hipError_t launch_bwd_dq_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+template <class T, int D>
+static hipError_t launch_bwd_dq_t(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
   if (!p.cu_q && causal && FAL_BWD_DQ_PAIR)
     grid.x = (unsigned)((cdiv(p.Nq, kDqNW * 32) + 1) / 2) * p.B * p.Hq;
   if (causal)
-    hipLaunchKernelGGL((bwd_dq_kernel<D, kDqNW, FAL_BWD_DQ_BN, true>), grid, dim3(kDqNW * 64), 0, st, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, kDqNW, FAL_BWD_DQ_BN, true>), grid, dim3(kDqNW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((bwd_dq_kernel<D, kDqNW, FAL_BWD_DQ_BN, false>), grid, dim3(kDqNW * 64), 0, st, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, kDqNW, FAL_BWD_DQ_BN, false>), grid, dim3(kDqNW * 64), 0, st, p);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_bwd_dq_d(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+  return p.bf16 ? launch_bwd_dq_t<bf16_t, D>(p, causal, grid, st) : launch_bwd_dq_t<half_t, D>(p, causal, grid, st);
 }
 
 hipError_t launch_bwd_dq(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st) {
@@ -1062,17 +1088,22 @@ hipError_t launch_bwd(const BwdParams& p, int d, int causal, dim3 grid, hipStrea
   }
 }
 
-template <int D, bool PRE>
-static hipError_t launch_rowwise(const BwdParams& p, int batched, hipStream_t st) {
+template <class T, int D, bool PRE>
+static hipError_t launch_rowwise_t(const BwdParams& p, int batched, hipStream_t st) {
   const int rows = batched ? p.B * p.Hq * p.Nq : p.total_q * p.Hq;
   if (rows == 0) return hipSuccess;
   constexpr int RPB = 256 / row_group<D>();
   dim3 grid(cdiv(rows, RPB));
   if (PRE)
-    hipLaunchKernelGGL((bwd_pre_kernel<D>), grid, dim3(256), 0, st, p, rows, batched);
+    hipLaunchKernelGGL((bwd_pre_kernel<T, D>), grid, dim3(256), 0, st, p, rows, batched);
   else
-    hipLaunchKernelGGL((bwd_post_kernel<D>), grid, dim3(256), 0, st, p, rows, batched);
+    hipLaunchKernelGGL((bwd_post_kernel<T, D>), grid, dim3(256), 0, st, p, rows, batched);
   return hipGetLastError();
+}
+
+template <int D, bool PRE>
+static hipError_t launch_rowwise(const BwdParams& p, int batched, hipStream_t st) {
+  return p.bf16 ? launch_rowwise_t<bf16_t, D, PRE>(p, batched, st) : launch_rowwise_t<half_t, D, PRE>(p, batched, st);
 }
 
 hipError_t launch_bwd_pre(const BwdParams& p, int d, int batched, hipStream_t st) {

@@ -32,6 +32,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -105,8 +106,96 @@ __device__ __forceinline__ half8 cvt8(const f32x16& c, int t) {
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// ---- element-type generic forms (fp16 or bf16 operands, fp32 accumulation) ----
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <class T> struct ElemVec;
+template <> struct ElemVec<half_t> { typedef half8 v8; typedef half4 v4; };
+template <> struct ElemVec<bf16_t> { typedef bf16x8 v8; typedef bf16x4 v4; };
+template <class T> using vec8 = typename ElemVec<T>::v8;
+template <class T> using vec4 = typename ElemVec<T>::v4;
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 8 consecutive elements (16 bytes) at p
+template <class T>
+__device__ __forceinline__ vec8<T> ld8(const T* p) {
+  return __builtin_bit_cast(vec8<T>, *reinterpret_cast<const u32x4*>(p));
+}
+template <class T>
+__device__ __forceinline__ vec8<T> zero8() {
+  return __builtin_bit_cast(vec8<T>, u32x4{0, 0, 0, 0});
+}
+// two 4-element halves joined into the 8 k-slots of an MFMA operand
+__device__ __forceinline__ half8 join8(half4 lo, half4 hi) {
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+__device__ __forceinline__ bf16x8 join8(bf16x4 lo, bf16x4 hi) {
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// transposed LDS read of 16-bit elements (see lds_read_tr), typed by the tile's element
+template <class T>
+__device__ __forceinline__ vec4<T> lds_tr(const T* p) {
+  typedef __attribute__((address_space(3))) short4v lds_s4;
+  short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
+  return __builtin_bit_cast(vec4<T>, v);
+}
+// elements 8t..8t+7 of an accumulator, rounded to T
+template <class T>
+__device__ __forceinline__ vec8<T> cvt8t(const f32x16& c, int t) {
+  vec8<T> r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = (T)c[8 * t + j];
+  return r;
+}
+// sum of 8 elements into an fp32 accumulator (dot2 with ones)
+__device__ __forceinline__ float sum8(half8 v, float acc) {
+  const half2v one = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2(half2v{v[2 * j], v[2 * j + 1]}, one, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
+  const bf16x2 one = {(bf16_t)1.f, (bf16_t)1.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[2 * j], v[2 * j + 1]}, one, acc, false);
+  return acc;
+}
+// A/B operand (8 k-slots) of rows row0.. of a row-major tile (see lds_kslab_tr)
+template <class T>
+__device__ __forceinline__ vec8<T> kslab_tr(const T* base, int row0, int hh, int ld) {
+  return join8(lds_tr(base + (row0 + hh * 4) * ld), lds_tr(base + (row0 + 8 + hh * 4) * ld));
+}
+__device__ __forceinline__ u32x4 ld_u4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st_u4(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+// acc + sum_j a[j] * b[j] over 8 elements
+__device__ __forceinline__ float dot8(half8 a, half8 b, float acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc = __builtin_amdgcn_fdot2(half2v{a[2 * j], a[2 * j + 1]}, half2v{b[2 * j], b[2 * j + 1]}, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{a[2 * j], a[2 * j + 1]}, bf16x2{b[2 * j], b[2 * j + 1]}, acc,
+                                          false);
+  return acc;
+}
+
 // Sum of 8 fp16 values into an fp32 accumulator (v_dot2 with ones).
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float sum8_f16(half8 v, float acc) {
   const half2v one = {(half_t)1.f, (half_t)1.f};
 #pragma unroll
@@ -117,7 +206,7 @@ __device__ __forceinline__ float sum8_f16(half8 v, float acc) {
 // 16-byte global -> LDS copy that bypasses VGPRs (gfx950 global_load_lds_dwordx4).
 // Lane i of the wave writes bytes [16 i, 16 i + 16) of `lds_wave_base`, which must be
 // the same for all lanes.  Completion is tracked by vmcnt (see wait_vmcnt0).
-__device__ __forceinline__ void global_to_lds16(const half_t* src, half_t* lds_wave_base) {
+__device__ __forceinline__ void global_to_lds16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
                                    (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
 }
@@ -129,7 +218,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // [16 i, 16 i + 16) of `lds_wave_base` (uniform across the wave).
 // AUX: cache-policy bits of the load.
 template <int AUX = 0>
-__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rs, int voffset, half_t* lds_wave_base) {
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rs, int voffset, void* lds_wave_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds_wave_base), 16,
                                            voffset, 0, 0, AUX);
 }

@@ -37,9 +37,6 @@ namespace fal {
 #define FAL_DEC_VAUX 2   // cache-policy bits of the V loads: nt (read once, evict first)
 #endif
 
-__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
@@ -62,7 +59,7 @@ __device__ __forceinline__ int vswz(int r) {
   return D == 96 ? (r & 3) : (r & ((D / 8 < 16 ? D / 8 : 16) - 1));
 }
 
-template <int D, int NW>
+template <class T, int D, int NW>
 __global__ void __launch_bounds__(NW * 64)
 decode_split_kernel(DecodeParams p) {
   constexpr int KS = D / 32;              // 16x16x32 k-steps over the head dim
@@ -72,7 +69,8 @@ decode_split_kernel(DecodeParams p) {
   constexpr int VI = 16 * CPR / 64;       // direct loads per V slice
   constexpr int LPS = 2 * KS + 2 * VI;    // loads issued per 32-row step
   static_assert(16 * CPR % 64 == 0, "slice must be whole load instructions");
-  __shared__ __attribute__((aligned(1024))) half_t vsm[NW][4 * SLICE];   // 2 steps x 2 slices
+  using V8 = vec8<T>;
+  __shared__ __attribute__((aligned(1024))) T vsm[NW][4 * SLICE];   // 2 steps x 2 slices
   __shared__ float m_s[NW][16];
   __shared__ float l_s[NW][16];
   __shared__ float inv_s[16];
@@ -102,8 +100,8 @@ decode_split_kernel(DecodeParams p) {
   const int nh = min(16, G - hg * 16);
 
 
-  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
-  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
+  const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
+  const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
   // K: lane loads row l16, columns t*32 + g4*8 .. +8 of each slice (A operand layout)
   const int kvo = (int)(l16 * p.k_ss + g4 * 8) * 2;
   // V: load instruction I of a slice fills chunks [I*64, I*64+64)
@@ -115,10 +113,10 @@ decode_split_kernel(DecodeParams p) {
     const int cch = (pch % CPR) ^ vswz<D>(r);
     vvo[I] = (int)(r * p.v_ss + cch * 8) * 2;
   }
-  half_t* vring = &vsm[ws][0];
+  T* vring = &vsm[ws][0];
 
   // one 32-row step = two 16-row slices
-  half8 kreg[2][2][KS];
+  V8 kreg[2][2][KS];
   auto issue = [&](int step, int buf) {
     const int r0 = k_begin + step * 32;
 #pragma unroll
@@ -131,7 +129,7 @@ decode_split_kernel(DecodeParams p) {
           make_rsrc(vbase + (int64_t)rs * p.v_ss, (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
       for (int t = 0; t < KS; ++t)
-        kreg[buf][sl][t] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo + t * 64, 0, 0));
+        kreg[buf][sl][t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo + t * 64, 0, 0));
 #pragma unroll
       for (int I = 0; I < VI; ++I)
         buffer_to_lds16<FAL_DEC_VAUX>(vrs, vvo[I], vring + (buf * 2 + sl) * SLICE + I * 64 * 8);
@@ -143,11 +141,11 @@ decode_split_kernel(DecodeParams p) {
   if (j + NW < nsteps) issue(j + NW, 1);
 
   // queries of the head tile as the B operand (n = head, k = head dim)
-  half8 qreg[KS];
-  const half_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)(hbase + l16) * p.q_sh;
+  V8 qreg[KS];
+  const T* qrow = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)(hbase + l16) * p.q_sh;
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    qreg[t] = l16 < nh ? load_h8(qrow + t * 32 + g4 * 8) : zero_h8();
+    qreg[t] = l16 < nh ? ld8(qrow + t * 32 + g4 * 8) : zero8<T>();
     if (p.negate_q) qreg[t] = -qreg[t];
   }
   const float c = p.scale_log2;
@@ -195,21 +193,19 @@ decode_split_kernel(DecodeParams p) {
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
     m_run = m_new;
-    half8 pb;
+    V8 pb;
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pb[sl * 4 + i] = (half_t)fast_exp2(s[sl][i] - m_use);
-    l_run = sum8_f16(pb, l_run * alpha);
+      for (int i = 0; i < 4; ++i) pb[sl * 4 + i] = (T)fast_exp2(s[sl][i] - m_use);
+    l_run = sum8(pb, l_run * alpha);
 #pragma unroll
     for (int db = 0; db < DBN; ++db) oacc[db] *= alpha;
     // O^T += V^T P^T over the 32 rows
-    const half_t* v0 = vring + (buf * 2) * SLICE;
+    const T* v0 = vring + (buf * 2) * SLICE;
 #pragma unroll
     for (int db = 0; db < DBN; ++db) {
-      const half4 lo = lds_read_tr(v0 + VRD(db));
-      const half4 hi = lds_read_tr(v0 + SLICE + VRD(db));
-      oacc[db] = mfma16(half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pb, oacc[db]);
+      oacc[db] = mfma16(join8(lds_tr(v0 + VRD(db)), lds_tr(v0 + SLICE + VRD(db))), pb, oacc[db]);
     }
     // LDS reads of this buffer must finish before the next loads overwrite it
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -265,7 +261,7 @@ decode_split_kernel(DecodeParams p) {
 
 // One wave per (sequence, query head): merge the splits' partial outputs, sixteen splits
 // per round trip.
-template <int D>
+template <class T, int D>
 __global__ void __launch_bounds__(64)
 decode_combine_kernel(DecodeParams p) {
   const int hq = blockIdx.x;
@@ -311,11 +307,11 @@ decode_combine_kernel(DecodeParams p) {
     M = Mn;
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  half_t* orow = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
+  T* orow = (T*)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh;
 #pragma unroll
   for (int j = 0; j < DJ; ++j) {
     const int d = lane + 64 * j;
-    if (d < D) orow[d] = (half_t)(acc[j] * inv);
+    if (d < D) orow[d] = (T)(acc[j] * inv);
   }
   if (p.lse && lane == 0)
     p.lse[(int64_t)b * p.Hq + hq] = (wsum > 0.f && M != -INFINITY) ? (M + fast_log2(wsum)) * kLn2 : -INFINITY;
@@ -379,20 +375,25 @@ int decode_chunk(int d, int B, int Hkv, int max_seqlen) {
   return chunk < tile ? tile : chunk;
 }
 
-template <int D>
-static hipError_t launch_decode_d(const DecodeParams& p, hipStream_t st) {
+template <class T, int D>
+static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t st) {
   const int nhg = cdiv(p.Hq / p.Hkv, 16);
   const int capacity = p.B * p.max_splits;
   hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(1024), 0, st, p.seqlens, p.B, p.max_seqlen, p.chunk,
                      const_cast<int2*>(p.work), capacity);
   hipError_t e0 = hipGetLastError();
   if (e0 != hipSuccess) return e0;
-  hipLaunchKernelGGL((decode_split_kernel<D, FAL_DEC_NW>), dim3((unsigned)capacity * p.Hkv * nhg),
+  hipLaunchKernelGGL((decode_split_kernel<T, D, FAL_DEC_NW>), dim3((unsigned)capacity * p.Hkv * nhg),
                      dim3(FAL_DEC_NW * 64), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(p.Hq, p.B), dim3(64), 0, st, p);
+  hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(p.Hq, p.B), dim3(64), 0, st, p);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_decode_d(const DecodeParams& p, hipStream_t st) {
+  return p.bf16 ? launch_decode_t<bf16_t, D>(p, st) : launch_decode_t<half_t, D>(p, st);
 }
 
 hipError_t launch_decode(const DecodeParams& p, int d, hipStream_t st) {

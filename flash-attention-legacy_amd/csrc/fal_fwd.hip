@@ -88,11 +88,16 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
   return true;
 }
 
-template <int D, int NW, int BN, bool CAUSAL, int RB>
+template <class T, int D, int NW, int BN, bool CAUSAL, int RB>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((RB == 2 && D >= 128) ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
 fwd_kernel(FwdParams p) {
   using TL = SwizzledTile<D>;
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
+  // fp16: Q is pre-multiplied by scale*log2(e) and rounded once (11-bit mantissa);
+  // bf16 keeps Q exact and scales the fp32 scores instead (one FMA per score)
+  constexpr bool PRESCALE = std::is_same<T, half_t>::value;
   constexpr int BM = NW * 32 * RB;  // query rows per workgroup (RB 32-row blocks per wave)
   constexpr int KS = D / 16;        // MFMA k-steps over the head dim
   constexpr int NKB = BN / 32;      // 32-key blocks per tile
@@ -102,7 +107,7 @@ fwd_kernel(FwdParams p) {
   constexpr int IPT = BN * CPR / (NW * 64);   // direct-to-LDS loads per wave per part
   static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(1024))) half_t smem[2 * 2 * PART];
+  __shared__ __attribute__((aligned(1024))) T smem[2 * 2 * PART];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -118,10 +123,10 @@ fwd_kernel(FwdParams p) {
   const int m0 = qt * BM;
   if (m0 >= nq) return;
 
-  const half_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
-  const half_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
-  const half_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
-  half_t* obase = p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)q_off * p.o_ss;
+  const T* qbase = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
+  const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
+  const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)k_off * p.v_ss;
+  T* obase = (T*)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)q_off * p.o_ss;
   float* lbase = p.lse + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
 
   // ---- Q slices of this wave into registers (B operand: n = query row, k = head dim) ----
@@ -130,15 +135,17 @@ fwd_kernel(FwdParams p) {
   // sign included), so the MFMA yields scores in the log2 domain directly.
   const float c = p.scale_log2;
   int row[RB];
-  half8 qreg[RB][KS];
+  V8 qreg[RB][KS];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     row[rb] = m0 + (w * RB + rb) * 32 + l32;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
-      half8 x = row[rb] < nq ? load_h8(qbase + (int64_t)row[rb] * p.q_ss + t * 16 + hh * 8) : zero_h8();
+      V8 x = row[rb] < nq ? ld8(qbase + (int64_t)row[rb] * p.q_ss + t * 16 + hh * 8) : zero8<T>();
+      if (PRESCALE) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = (half_t)((float)x[e] * c);
+        for (int e = 0; e < 8; ++e) x[e] = (T)((float)x[e] * c);
+      }
       qreg[rb][t] = x;
     }
   }
@@ -183,8 +190,8 @@ fwd_kernel(FwdParams p) {
   // past the end of the sequence read as zeros.
   auto load_tile = [&](int tile, int buf) {
     const int n0 = tile * BN;
-    half_t* kdst = smem + buf * 2 * PART;
-    half_t* vdst = kdst + PART;
+    T* kdst = smem + buf * 2 * PART;
+    T* vdst = kdst + PART;
     const int64_t left = (int64_t)max(nk - n0, 0);
     const __amdgpu_buffer_rsrc_t krs =
         make_rsrc(kbase + (int64_t)n0 * p.k_ss, (uint32_t)min(left * p.k_ss * 2, (int64_t)0x7fffffff));
@@ -219,31 +226,39 @@ fwd_kernel(FwdParams p) {
   auto tile_body = [&](auto masked, int j, int buf) {
     constexpr bool MASK = decltype(masked)::value;
     const int n0 = j * BN;
-    const half_t* ks = smem + buf * 2 * PART;
-    const half_t* vs = ks + PART;
+    const T* ks = smem + buf * 2 * PART;
+    const T* vs = ks + PART;
     // S^T = K Q^T, the 32-key blocks interleaved so consecutive MFMAs are independent.
     // K fragments are read FAL_FWD_KDEPTH k-steps ahead of the MFMAs that use them.
     f32x16 sacc[RB][NKB];
-    half8 kfrag[KS][NKB];
+    V8 kfrag[KS][NKB];
 #pragma unroll
     for (int t = 0; t < FAL_FWD_KDEPTH && t < KS; ++t)
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) kfrag[t][kb] = load_h8(ks + kaddr[t] + kb * 32 * CPR * 8);
+      for (int kb = 0; kb < NKB; ++kb) kfrag[t][kb] = ld8(ks + kaddr[t] + kb * 32 * CPR * 8);
     __builtin_amdgcn_sched_group_barrier(0x100, (FAL_FWD_KDEPTH < KS ? FAL_FWD_KDEPTH : KS) * NKB, 0);
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       if (t + FAL_FWD_KDEPTH < KS) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
-          kfrag[t + FAL_FWD_KDEPTH][kb] = load_h8(ks + kaddr[t + FAL_FWD_KDEPTH] + kb * 32 * CPR * 8);
+          kfrag[t + FAL_FWD_KDEPTH][kb] = ld8(ks + kaddr[t + FAL_FWD_KDEPTH] + kb * 32 * CPR * 8);
         __builtin_amdgcn_sched_group_barrier(0x100, NKB, 0);   // the reads ...
       }
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          sacc[rb][kb] = mfma32(kfrag[t][kb], qreg[rb][t], t == 0 ? negm[rb] : sacc[rb][kb]);
+          sacc[rb][kb] = mfma32(kfrag[t][kb], qreg[rb][t], t == 0 ? (PRESCALE ? negm[rb] : zero_f16()) : sacc[rb][kb]);
       __builtin_amdgcn_sched_group_barrier(0x008, NKB * RB, 0);  // ... then the MFMAs of step t
+    }
+    if (!PRESCALE) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[rb][kb][i] = fmaf(sacc[rb][kb][i], c, negm[rb][i]);
     }
     if (MASK) {
 #pragma unroll
@@ -258,7 +273,7 @@ fwd_kernel(FwdParams p) {
     }
     // P^T = exp2(s - m_run) in fp16 (the B operand of O^T += V^T P^T) and this tile's
     // per-lane p sum
-    half8 pb[RB][NKB][2];
+    V8 pb[RB][NKB][2];
     float lt[RB];
     auto make_p = [&]() {
 #pragma unroll
@@ -268,11 +283,11 @@ fwd_kernel(FwdParams p) {
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int t2 = 0; t2 < 2; ++t2) {
-            half8 h;
+            V8 h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (half_t)fast_exp2(sacc[rb][kb][t2 * 8 + e]);
+            for (int e = 0; e < 8; ++e) h[e] = (T)fast_exp2(sacc[rb][kb][t2 * 8 + e]);
             pb[rb][kb][t2] = h;
-            lt[rb] = sum8_f16(h, lt[rb]);
+            lt[rb] = sum8(h, lt[rb]);
           }
       }
     };
@@ -324,9 +339,7 @@ fwd_kernel(FwdParams p) {
         const int kofs = (kb * 2 + t2) * 16 * CPR * 8;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const half4 lo = lds_read_tr(vs + vaddr[0][db] + kofs);
-          const half4 hi = lds_read_tr(vs + vaddr[1][db] + kofs);
-          const half8 va = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const V8 va = join8(lds_tr(vs + vaddr[0][db] + kofs), lds_tr(vs + vaddr[1][db] + kofs));
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) oacc[rb][db] = mfma32(va, pb[rb][kb][t2], oacc[rb][db]);
         }
@@ -368,15 +381,15 @@ fwd_kernel(FwdParams p) {
     const float l_tot = pair_sum(l_run[rb]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (row[rb] < nq) {
-      half_t* orow = obase + (int64_t)row[rb] * p.o_ss;
+      T* orow = obase + (int64_t)row[rb] * p.o_ss;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          half4 h;
+          V4 h;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = (half_t)(oacc[rb][db][g4 * 4 + e] * inv);
-          *reinterpret_cast<half4*>(orow + db * 32 + g4 * 8 + hh * 4) = h;
+          for (int e = 0; e < 4; ++e) h[e] = (T)(oacc[rb][db][g4 * 4 + e] * inv);
+          *reinterpret_cast<V4*>(orow + db * 32 + g4 * 8 + hh * 4) = h;
         }
       if (hh == 0) {
         float L = -INFINITY;
@@ -461,14 +474,18 @@ struct FwdCfg {
   static constexpr int RB = D == 128 ? FAL_FWD_RB128 : D == 32 ? FAL_FWD_RB32 : D == 64 ? FAL_FWD_RB64 : 1;
 };
 
-template <int D>
-static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
+template <class T, int D>
+static hipError_t launch_fwd_t(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
   constexpr int NW = FwdCfg<D>::NW, BN = FwdCfg<D>::BN, RB = FwdCfg<D>::RB;
   if (causal)
-    hipLaunchKernelGGL((fwd_kernel<D, NW, BN, true, RB>), grid, dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((fwd_kernel<T, D, NW, BN, true, RB>), grid, dim3(NW * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((fwd_kernel<D, NW, BN, false, RB>), grid, dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((fwd_kernel<T, D, NW, BN, false, RB>), grid, dim3(NW * 64), 0, st, p);
   return hipGetLastError();
+}
+template <int D>
+static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
+  return p.bf16 ? launch_fwd_t<bf16_t, D>(p, causal, grid, st) : launch_fwd_t<half_t, D>(p, causal, grid, st);
 }
 
 template <int D>

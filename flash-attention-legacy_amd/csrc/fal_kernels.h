@@ -30,6 +30,7 @@ struct FwdParams {
   const int* cu_q;
   const int* cu_k;
   const int2* work;
+  int bf16;           // element type of every fp16/bf16 tensor: 0 fp16, 1 bf16
 };
 
 // Backward.  Same addressing as FwdParams, plus dO (do_*), the fp32 dQ
@@ -68,6 +69,7 @@ struct BwdParams {
   int n_qitems;       // capacity of qwork
   int total_q;        // varlen: rows of the packed Q (row-wise kernels)
   int total_k;        // varlen: rows of the packed K/V
+  int bf16;           // element type of every fp16/bf16 tensor: 0 fp16, 1 bf16
 };
 
 // KV-cache decode (one query token per sequence).
@@ -91,6 +93,7 @@ struct DecodeParams {
   int max_seqlen;           // cache rows; cache_seqlens are clamped to it
   float scale_log2;
   int negate_q;
+  int bf16;           // element type of every fp16/bf16 tensor: 0 fp16, 1 bf16
 };
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);

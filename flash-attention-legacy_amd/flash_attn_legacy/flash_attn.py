@@ -19,6 +19,8 @@ from torch.autograd import Function
 from . import hip_ext as _ext
 
 _HEAD_DIMS = (32, 64, 96, 128, 256)
+# float16 as in the reference; bfloat16 runs natively as well (bf16 MFMA, fp32 accumulation)
+_DTYPES = (torch.float16, torch.bfloat16)
 
 
 class FlashAttentionFunc(Function):
@@ -27,8 +29,8 @@ class FlashAttentionFunc(Function):
 
     @staticmethod
     def forward(ctx, q, k, v, softmax_scale, is_causal):
-        assert q.dtype == torch.float16, f"Q must be float16, got {q.dtype}"
-        assert k.dtype == torch.float16 and v.dtype == torch.float16
+        assert q.dtype in _DTYPES, f"Q must be float16 or bfloat16, got {q.dtype}"
+        assert k.dtype == q.dtype and v.dtype == q.dtype
         assert q.is_cuda and q.dim() == 4
         d = q.shape[-1]
         assert d in _HEAD_DIMS, f"head_dim must be 32, 64, 96, 128, or 256, got {d}"
@@ -66,14 +68,14 @@ def flash_attention(
       - MQA: GQA with H_kv = 1
 
     Args:
-        q: Query [B, H_q, N, d] float16
-        k: Key   [B, H_kv, N, d] float16
-        v: Value [B, H_kv, N, d] float16
+        q: Query [B, H_q, N, d] float16 or bfloat16
+        k: Key   [B, H_kv, N, d], same dtype
+        v: Value [B, H_kv, N, d], same dtype
         softmax_scale: default 1/sqrt(d)
         is_causal: causal mask (top-left aligned: key j visible to query i iff j <= i)
 
     Returns:
-        [B, H_q, N, d] float16
+        [B, H_q, N, d], dtype of q
     """
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
@@ -88,7 +90,8 @@ class FlashAttnVarlenFunc(Function):
     @staticmethod
     def forward(ctx, q, k, v, cu_seqlens_q, cu_seqlens_k,
                 max_seqlen_q, max_seqlen_k, softmax_scale, is_causal):
-        assert q.dtype == torch.float16, f"Q must be float16, got {q.dtype}"
+        assert q.dtype in _DTYPES, f"Q must be float16 or bfloat16, got {q.dtype}"
+        assert k.dtype == q.dtype and v.dtype == q.dtype
         assert q.is_cuda and q.dim() == 3
         d = q.shape[-1]
         assert d in _HEAD_DIMS, f"head_dim must be 32, 64, 96, 128, or 256, got {d}"
@@ -134,7 +137,7 @@ def flash_attn_varlen_func(
     uses per-sequence (local) indices.
 
     Args:
-        q: [total_q, num_heads, head_dim] float16
+        q: [total_q, num_heads, head_dim] float16 or bfloat16
         k: [total_k, num_heads_k, head_dim] float16
         v: [total_k, num_heads_k, head_dim] float16
         cu_seqlens_q: [batch_size + 1] int32 cumulative sequence lengths for Q
@@ -145,12 +148,12 @@ def flash_attn_varlen_func(
         causal: apply causal mask
 
     Returns:
-        [total_q, num_heads, head_dim] float16
+        [total_q, num_heads, head_dim], dtype of q
     """
     assert q.dim() == 3, f"q must be [total, heads, d], got shape {q.shape}"
     assert k.dim() == 3, f"k must be [total, heads_k, d], got shape {k.shape}"
     assert v.dim() == 3, f"v must be [total, heads_k, d], got shape {v.shape}"
-    assert q.dtype == torch.float16, f"Q must be float16, got {q.dtype}"
+    assert q.dtype in _DTYPES, f"Q must be float16 or bfloat16, got {q.dtype}"
 
     d = q.shape[-1]
     assert d in _HEAD_DIMS, f"head_dim must be 32, 64, 96, 128, or 256, got {d}"
@@ -181,7 +184,7 @@ def flash_attn_with_kvcache(
     (reference integrations.py:77-98).  Results match that formula.
 
     Args:
-        q: [B, 1, H_q, d] float16 (or [B, H_q, d])
+        q: [B, 1, H_q, d] float16 or bfloat16 (or [B, H_q, d])
         k_cache, v_cache: [B, S_max, H_kv, d] float16 (``cache_layout="bshd"``) or
             [B, H_kv, S_max, d] (``"bhsd"``, the HF layout)
         cache_seqlens: int32 tensor [B] (or an int for all sequences)
@@ -194,7 +197,7 @@ def flash_attn_with_kvcache(
     squeeze = q.dim() == 3
     q3 = q if squeeze else q.reshape(q.shape[0], q.shape[2], q.shape[3]) if q.shape[1] == 1 else None
     assert q3 is not None, "flash_attn_with_kvcache supports one query token per sequence"
-    assert q.dtype == torch.float16, f"q must be float16, got {q.dtype}"
+    assert q.dtype in _DTYPES, f"q must be float16 or bfloat16, got {q.dtype}"
     d = q3.shape[-1]
     assert d in _HEAD_DIMS, f"head_dim must be 32, 64, 96, 128, or 256, got {d}"
     if softmax_scale is None:
@@ -277,12 +280,12 @@ class FlashMultiHeadAttention(nn.Module):
         v = self.v_proj(kv).view(B, -1, self.num_kv_heads, self.head_dim).transpose(1, 2)
 
         orig_dtype = q.dtype
-        if q.dtype != torch.float16:
+        if q.dtype not in _DTYPES:
             q, k, v = q.half(), k.half(), v.half()
 
         out = flash_attention(q, k, v, self.scale, self.causal)
 
-        if orig_dtype != torch.float16:
+        if orig_dtype != out.dtype:
             out = out.to(orig_dtype)
 
         out = out.transpose(1, 2).contiguous().view(B, N, self.embed_dim)

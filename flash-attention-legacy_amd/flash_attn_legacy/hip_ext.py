@@ -63,6 +63,8 @@ def _load() -> ctypes.CDLL:
         "fal_decode_workspace_size": (_SZ, [_I64] * 5),
         "fal_decode": (_INT, [_VP] * 5 + [_I64, _VP, _VP] + [_I64] * 5 + [_STR] * 4 + [_F32, _VP, _SZ, _VP]),
     }
+    for name in ("fal_fwd", "fal_fwd_varlen", "fal_bwd", "fal_bwd_varlen", "fal_decode"):
+        sig[name + "_bf16"] = sig[name]   # bf16 forms: same arguments
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
         fn.restype = res
@@ -78,6 +80,7 @@ SYMBOLS = (
     "fal_fwd", "fal_fwd_varlen_workspace_size", "fal_fwd_varlen",
     "fal_bwd_workspace_size", "fal_bwd", "fal_bwd_varlen_workspace_size", "fal_bwd_varlen",
     "fal_decode_workspace_size", "fal_decode",
+    "fal_fwd_bf16", "fal_fwd_varlen_bf16", "fal_bwd_bf16", "fal_bwd_varlen_bf16", "fal_decode_bf16",
 )
 
 
@@ -148,11 +151,23 @@ def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
 
 
-def _check_half_cuda(name: str, t: torch.Tensor) -> None:
+DTYPES = (torch.float16, torch.bfloat16)
+
+
+def _check_half_cuda(name: str, t: torch.Tensor, dtype: Optional[torch.dtype] = None) -> None:
+    """t is a CUDA tensor of dtype (or, with dtype None, of float16 or bfloat16)."""
     if not t.is_cuda:
         raise RuntimeError(f"{name} must be on CUDA")
-    if t.dtype != torch.float16:
-        raise RuntimeError(f"{name} must be float16")
+    if dtype is None:
+        if t.dtype not in DTYPES:
+            raise RuntimeError(f"{name} must be float16 or bfloat16")
+    elif t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {str(dtype)[6:]} like Q")
+
+
+def _fn(name: str, dtype: torch.dtype):
+    """The library entry point for an element type (fp16, or its _bf16 form)."""
+    return getattr(_lib, name + "_bf16") if dtype == torch.bfloat16 else getattr(_lib, name)
 
 
 # ---------------------------------------------------------------------------
@@ -168,8 +183,8 @@ def forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, softmax_scale: fl
         raise RuntimeError("Q must be [B, H_q, N, d]")
     if K.dim() != 4 or V.dim() != 4:
         raise RuntimeError("K,V must be 4D")
-    _check_half_cuda("K", K)
-    _check_half_cuda("V", V)
+    _check_half_cuda("K", K, Q.dtype)
+    _check_half_cuda("V", V, Q.dtype)
     B, Hq, N, d = Q.shape
     Hkv, Nk = K.shape[1], K.shape[2]
     if K.shape[0] != B or K.shape[3] != d:
@@ -178,12 +193,13 @@ def forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, softmax_scale: fl
         raise RuntimeError("V shape mismatch")
     Q, K, V = _usable(Q), _usable(K), _usable(V)
     dev = Q.device
-    O = torch.empty((B, Hq, N, d), dtype=torch.float16, device=dev)
+    O = torch.empty((B, Hq, N, d), dtype=Q.dtype, device=dev)
     L = torch.empty((B, Hq, N), dtype=torch.float32, device=dev)
     arr, (qs, ks, vs, os_) = _stride_block(Q, K, V, O)
-    _check(_run(dev, lambda: _lib.fal_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), L.data_ptr(),
-                                          B, Hq, Hkv, N, Nk, d, qs, ks, vs, os_, float(softmax_scale),
-                                          int(bool(is_causal)), _raw_stream(dev.index))))
+    fwd = _fn("fal_fwd", Q.dtype)
+    _check(_run(dev, lambda: fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), L.data_ptr(),
+                                 B, Hq, Hkv, N, Nk, d, qs, ks, vs, os_, float(softmax_scale),
+                                 int(bool(is_causal)), _raw_stream(dev.index))))
     return [O, L]
 
 
@@ -197,6 +213,8 @@ def forward_varlen(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_s
         raise RuntimeError("Q must be [total_q, H_q, d]")
     if K.dim() != 3 or V.dim() != 3:
         raise RuntimeError("K,V must be 3D")
+    _check_half_cuda("K", K, Q.dtype)
+    _check_half_cuda("V", V, Q.dtype)
     if cu_seqlens_q.dtype != torch.int32:
         raise RuntimeError("cu_seqlens_q must be int32")
     if cu_seqlens_k.dtype != torch.int32:
@@ -213,24 +231,23 @@ def forward_varlen(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_s
     Q, K, V = _usable(Q), _usable(K), _usable(V)
     cu_q = cu_seqlens_q.to(Q.device).contiguous()
     cu_k = cu_seqlens_k.to(Q.device).contiguous()
-    O = torch.empty((total_q, Hq, d), dtype=torch.float16, device=Q.device)
+    O = torch.empty((total_q, Hq, d), dtype=Q.dtype, device=Q.device)
     L = torch.empty((total_q, Hq), dtype=torch.float32, device=Q.device)
     ws = _workspace(_lib.fal_fwd_varlen_workspace_size(num_seqs, total_q, int(max_seqlen_q), d), Q.device)
     with torch.cuda.device(Q.device):
-        _check(_lib.fal_fwd_varlen(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(cu_q), _ptr(cu_k),
-                                   num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
-                                   _strides(Q, (None, 1, 0)), _strides(K, (None, 1, 0)),
-                                   _strides(V, (None, 1, 0)), _strides(O, (None, 1, 0)),
-                                   float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(),
-                                   _stream(Q.device)))
+        _check(_fn("fal_fwd_varlen", Q.dtype)(
+            _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(cu_q), _ptr(cu_k),
+            num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
+            _strides(Q, (None, 1, 0)), _strides(K, (None, 1, 0)), _strides(V, (None, 1, 0)), _strides(O, (None, 1, 0)),
+            float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(), _stream(Q.device)))
     return [O, L]
 
 
 def backward(dO, Q, K, V, O, L, softmax_scale: float, is_causal: bool = False) -> List[torch.Tensor]:
     """[dQ, dK, dV] from the saved forward (O, L).  Checks of ``flash_attn_backward``
     (csrc/flash_attn_legacy.cpp:115-120); dQ has Q's shape, dK/dV have K/V's."""
-    if not (Q.is_cuda and Q.dtype == torch.float16):
-        raise RuntimeError("Q must be CUDA float16")
+    if not (Q.is_cuda and Q.dtype in DTYPES):
+        raise RuntimeError("Q must be CUDA float16 or bfloat16")
     if dO.shape != Q.shape:
         raise RuntimeError("dO shape must match Q")
     B, Hq, N, d = Q.shape
@@ -238,20 +255,20 @@ def backward(dO, Q, K, V, O, L, softmax_scale: float, is_causal: bool = False) -
     if Hq % Hkv != 0:
         raise RuntimeError("H_q must be divisible by H_kv for GQA")
     for name, t in (("dO", dO), ("K", K), ("V", V), ("O", O)):
-        _check_half_cuda(name, t)
+        _check_half_cuda(name, t, Q.dtype)
     dO, Q, K, V, O = (_usable(t) for t in (dO, Q, K, V, O))
     L = L.contiguous()
-    dQ = torch.empty((B, Hq, N, d), dtype=torch.float16, device=Q.device)
-    dK = torch.empty((B, Hkv, Nk, d), dtype=torch.float16, device=Q.device)
-    dV = torch.empty((B, Hkv, Nk, d), dtype=torch.float16, device=Q.device)
+    dQ = torch.empty((B, Hq, N, d), dtype=Q.dtype, device=Q.device)
+    dK = torch.empty((B, Hkv, Nk, d), dtype=Q.dtype, device=Q.device)
+    dV = torch.empty((B, Hkv, Nk, d), dtype=Q.dtype, device=Q.device)
     ws = _workspace(_lib.fal_bwd_workspace_size(B, Hq, N, d), Q.device)
     with torch.cuda.device(Q.device):
-        _check(_lib.fal_bwd(_ptr(dO), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(dQ), _ptr(dK), _ptr(dV),
-                            B, Hq, Hkv, N, Nk, d,
-                            _strides(dO), _strides(Q), _strides(K), _strides(V), _strides(O),
-                            _strides(dQ), _strides(dK), _strides(dV),
-                            float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(),
-                            _stream(Q.device)))
+        _check(_fn("fal_bwd", Q.dtype)(
+            _ptr(dO), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(dQ), _ptr(dK), _ptr(dV),
+            B, Hq, Hkv, N, Nk, d,
+            _strides(dO), _strides(Q), _strides(K), _strides(V), _strides(O),
+            _strides(dQ), _strides(dK), _strides(dV),
+            float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(), _stream(Q.device)))
     return [dQ, dK, dV]
 
 
@@ -264,8 +281,10 @@ def backward_varlen(dO, Q, K, V, O, L, cu_seqlens_q, cu_seqlens_k, max_seqlen_q:
     """[dQ, dK, dV] for packed sequences in one launch.  Same results as the reference's
     per-sequence loop (flash_attn_legacy/flash_attn.py:133-157): dK/dV rows outside every
     segment are zero."""
-    if not (Q.is_cuda and Q.dtype == torch.float16):
-        raise RuntimeError("Q must be CUDA float16")
+    if not (Q.is_cuda and Q.dtype in DTYPES):
+        raise RuntimeError("Q must be CUDA float16 or bfloat16")
+    for name, t in (("dO", dO), ("K", K), ("V", V), ("O", O)):
+        _check_half_cuda(name, t, Q.dtype)
     if dO.shape != Q.shape:
         raise RuntimeError("dO shape must match Q")
     total_q, Hq, d = Q.shape
@@ -275,18 +294,17 @@ def backward_varlen(dO, Q, K, V, O, L, cu_seqlens_q, cu_seqlens_k, max_seqlen_q:
     L = L.contiguous()
     cu_q = cu_seqlens_q.to(device=Q.device, dtype=torch.int32).contiguous()
     cu_k = cu_seqlens_k.to(device=Q.device, dtype=torch.int32).contiguous()
-    dQ = torch.empty((total_q, Hq, d), dtype=torch.float16, device=Q.device)
-    dK = torch.zeros((total_k, Hkv, d), dtype=torch.float16, device=Q.device)
-    dV = torch.zeros((total_k, Hkv, d), dtype=torch.float16, device=Q.device)
+    dQ = torch.empty((total_q, Hq, d), dtype=Q.dtype, device=Q.device)
+    dK = torch.zeros((total_k, Hkv, d), dtype=Q.dtype, device=Q.device)
+    dV = torch.zeros((total_k, Hkv, d), dtype=Q.dtype, device=Q.device)
     ws = _workspace(_lib.fal_bwd_varlen_workspace_size(num_seqs, total_q, total_k, Hq, d), Q.device)
     st = lambda t: _strides(t, (None, 1, 0))
     with torch.cuda.device(Q.device):
-        _check(_lib.fal_bwd_varlen(_ptr(dO), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L),
-                                   _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(cu_q), _ptr(cu_k),
-                                   num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
-                                   st(dO), st(Q), st(K), st(V), st(O), st(dQ), st(dK), st(dV),
-                                   float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(),
-                                   _stream(Q.device)))
+        _check(_fn("fal_bwd_varlen", Q.dtype)(
+            _ptr(dO), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(dQ), _ptr(dK), _ptr(dV), _ptr(cu_q), _ptr(cu_k),
+            num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
+            st(dO), st(Q), st(K), st(V), st(O), st(dQ), st(dK), st(dV),
+            float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(), _stream(Q.device)))
     return [dQ, dK, dV]
 
 
@@ -296,8 +314,9 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_
     """Split-K decode.  q [B,Hq,d] (one token per sequence); caches [B,S,Hkv,d]
     (``cache_layout="bshd"``) or [B,Hkv,S,d] (``"bhsd"``); cache_seqlens int32 [B];
     mask_bias optional fp32 [B,S] additive mask.  Returns O [B,Hq,d] (and L [B,Hq])."""
-    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
-        _check_half_cuda(name, t)
+    _check_half_cuda("q", q)
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_half_cuda(name, t, q.dtype)
     if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise RuntimeError("decode expects q [B,Hq,d] and 4-D caches")
     B, Hq, d = q.shape
@@ -318,14 +337,13 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_
         bias = mask_bias.to(device=q.device, dtype=torch.float32)
         if bias.stride(-1) != 1:
             bias = bias.contiguous()
-    o = torch.empty((B, Hq, d), dtype=torch.float16, device=q.device)
+    o = torch.empty((B, Hq, d), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, Hq), dtype=torch.float32, device=q.device) if return_lse else None
     ws = _workspace(_lib.fal_decode_workspace_size(B, Hq, Hkv, S, d), q.device)
     with torch.cuda.device(q.device):
-        _check(_lib.fal_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(seqlens), _ptr(bias),
-                               bias.stride(0) if bias is not None else 0, _ptr(o), _ptr(lse),
-                               B, Hq, Hkv, d, S,
-                               _strides(q, (0, 1, None)), _strides(k_cache, cdims), _strides(v_cache, cdims),
-                               _strides(o, (0, 1, None)), float(softmax_scale), _ptr(ws), ws.numel(),
-                               _stream(q.device)))
+        _check(_fn("fal_decode", q.dtype)(
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(seqlens), _ptr(bias),
+            bias.stride(0) if bias is not None else 0, _ptr(o), _ptr(lse), B, Hq, Hkv, d, S,
+            _strides(q, (0, 1, None)), _strides(k_cache, cdims), _strides(v_cache, cdims),
+            _strides(o, (0, 1, None)), float(softmax_scale), _ptr(ws), ws.numel(), _stream(q.device)))
     return (o, lse) if return_lse else o

@@ -138,7 +138,9 @@ def flash_attn_legacy_forward(
         is_causal = False
 
     in_dtype = query.dtype
-    half = lambda t: t.half() if t.dtype != torch.float16 else t
+    # fp16 and bf16 run natively; other dtypes are cast to fp16 as in the reference
+    # (integrations.py:65-67)
+    half = lambda t: t if t.dtype in (torch.float16, torch.bfloat16) else t.half()
     attn_output = None
 
     if d in _HEAD_DIMS and q_len == kv_len and attention_mask is not None and attention_mask.dim() == 2:
@@ -164,7 +166,7 @@ def flash_attn_legacy_forward(
 
     if attn_output is None:
         attn_output = _eager(query, key, value, attention_mask, scaling, is_causal)
-    elif in_dtype != torch.float16:
+    elif attn_output.dtype != in_dtype:
         attn_output = attn_output.to(in_dtype)
 
     # [B, H, N, d] -> [B, N, H, d], the SDPA output layout

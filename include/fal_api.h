@@ -12,7 +12,8 @@
  *     csrc/flash_attn_legacy.cpp:48-60, csrc/include/flash_attn_common.h:297-305).
  *
  * Conventions
- *   - fp16 data (IEEE binary16), fp32 log-sum-exp, int32 sequence offsets.
+ *   - fp16 data (IEEE binary16; the *_bf16 entry points take bfloat16), fp32
+ *     log-sum-exp, int32 sequence offsets.
  *   - `*_strides` point at three int64 element strides (batch, head, seq) of a
  *     tensor whose last (head_dim) dimension is contiguous.  Packed (varlen)
  *     tensors use (unused, head, token).  Base pointers must be 16-byte aligned
@@ -156,6 +157,58 @@ int fal_decode(const void* q, const void* k_cache, const void* v_cache,
                const int64_t* q_strides, const int64_t* k_strides,
                const int64_t* v_strides, const int64_t* o_strides,
                float softmax_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * bf16 (bfloat16) forms of the five compute entry points: the same arguments,
+ * shapes, strides, workspace sizes and status codes, with every fp16 tensor
+ * (q, k, v, o, dout, dq, dk, dv, the caches) in bf16 instead; log-sum-exp, D and
+ * mask bias stay fp32.  Products accumulate in fp32 (bf16 MFMA); P and dS are
+ * rounded to bf16 for their second product, and the softmax scale is applied to
+ * the fp32 scores.  No counterpart in the reference, which is fp16 only (its HF
+ * integration casts bf16 models to fp16, integrations.py:65-67): this serves
+ * bf16 models without that cast and its overflow risk.
+ */
+int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                 int64_t batch, int64_t heads_q, int64_t heads_kv,
+                 int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
+                 const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 float softmax_scale, int is_causal, void* stream);
+int fal_fwd_varlen_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs,
+                        int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,
+                        int64_t head_dim, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                        const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides, const int64_t* o_strides,
+                        float softmax_scale, int is_causal,
+                        void* workspace, size_t workspace_bytes, void* stream);
+int fal_bwd_bf16(const void* dout, const void* q, const void* k, const void* v, const void* o,
+                 const float* lse, void* dq, void* dk, void* dv,
+                 int64_t batch, int64_t heads_q, int64_t heads_kv,
+                 int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
+                 const int64_t* do_strides, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+                 float softmax_scale, int is_causal,
+                 void* workspace, size_t workspace_bytes, void* stream);
+int fal_bwd_varlen_bf16(const void* dout, const void* q, const void* k, const void* v, const void* o,
+                        const float* lse, void* dq, void* dk, void* dv,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs,
+                        int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,
+                        int64_t head_dim, int64_t max_seqlen_q, int64_t max_seqlen_k,
+                        const int64_t* do_strides, const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides, const int64_t* o_strides,
+                        const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+                        float softmax_scale, int is_causal,
+                        void* workspace, size_t workspace_bytes, void* stream);
+int fal_decode_bf16(const void* q, const void* k_cache, const void* v_cache,
+                    const int32_t* cache_seqlens, const float* mask_bias, int64_t mask_stride,
+                    void* o, float* lse,
+                    int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                    int64_t max_seqlen_k,
+                    const int64_t* q_strides, const int64_t* k_strides,
+                    const int64_t* v_strides, const int64_t* o_strides,
+                    float softmax_scale, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }
