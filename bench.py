@@ -218,7 +218,7 @@ def main():
                    "seq_len": 4096, "head_dim": 128, "causal": True, "inputs": "fp16 N(0,1) seed 0"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                     "traffic": traffic, "kernel": "fwd_kernel<128,4,64,true,1>",
+                     "traffic": traffic, "kernel": "fwd_kernel<_Float16,128,4,64,true,1>",
                      "flops_per_launch": flops},
         "cpu_baseline": None if a.no_cpu else cpu_baseline(),
         "extra": extra,
