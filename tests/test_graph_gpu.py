@@ -13,7 +13,9 @@ from helpers import randn
 pytestmark = pytest.mark.gpu
 
 
-def replay_check(fn, eager_out, n=4):
+def replay_check(fn, eager_out, n=4, inexact=()):
+    """`inexact`: indices of outputs accumulated with atomics (d 256 dQ), compared to
+    within 1e-3 of their largest magnitude instead of bit for bit."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -32,6 +34,10 @@ def replay_check(fn, eager_out, n=4):
         g.replay()
         torch.cuda.synchronize()
         for idx, (got, ref) in enumerate(zip(outs, eager_out)):
+            if idx in inexact:
+                tol = 1e-3 * float(ref.float().abs().max())
+                assert float((got.float() - ref.float()).abs().max()) <= tol, f"replay {r}, output {idx}"
+                continue
             same = torch.equal(got, ref) or (torch.equal(torch.isnan(got), torch.isnan(ref)) and
                                              torch.equal(torch.nan_to_num(got), torch.nan_to_num(ref)))
             assert same, (f"replay {r}, output {idx}: nan {int(torch.isnan(got).sum())} vs "
@@ -40,17 +46,22 @@ def replay_check(fn, eager_out, n=4):
         del junk
 
 
-def test_graph_forward_backward():
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [128, 256])
+def test_graph_forward_backward(dtype, d):
+    """d 128 takes the split backward (two kernels), d 256 the atomic one (D and the
+    zeroed fp32 dQ accumulator from a kernel, the cast after it)."""
     from flash_attn_legacy import hip_ext
-    B, Hq, Hkv, N, d = 2, 8, 2, 384, 128
-    q, k, v, do = randn((B, Hq, N, d), seed=1), randn((B, Hkv, N, d), seed=2), randn((B, Hkv, N, d), seed=3), \
-        randn((B, Hq, N, d), seed=4)
+    B, Hq, Hkv, N = 2, 8, 2, 384
+    q, k, v, do = (randn(shape, seed=s).to(dtype) for shape, s in
+                   (((B, Hq, N, d), 1), ((B, Hkv, N, d), 2), ((B, Hkv, N, d), 3), ((B, Hq, N, d), 4)))
     scale = 1.0 / math.sqrt(d)
     o, lse = hip_ext.forward(q, k, v, scale, True)
     grads = hip_ext.backward(do, q, k, v, o, lse, scale, True)
     torch.cuda.synchronize()
     replay_check(lambda: tuple(hip_ext.forward(q, k, v, scale, True)), (o, lse))
-    replay_check(lambda: tuple(hip_ext.backward(do, q, k, v, o, lse, scale, True)), tuple(grads))
+    replay_check(lambda: tuple(hip_ext.backward(do, q, k, v, o, lse, scale, True)), tuple(grads),
+                 inexact=(0,) if d == 256 else ())
 
 
 def test_graph_varlen_and_decode():
