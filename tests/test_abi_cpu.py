@@ -38,6 +38,8 @@ def test_header_declares_the_expected_entry_points():
     for n in ("fal_fwd", "fal_fwd_varlen", "fal_bwd", "fal_bwd_varlen", "fal_decode",
               "fal_last_error", "fal_version", "fal_device_supported"):
         assert n in names
+    for n in ("fal_fwd", "fal_fwd_varlen", "fal_bwd", "fal_bwd_varlen", "fal_decode"):
+        assert n + "_bf16" in names
 
 
 def test_library_exports_every_header_symbol(ext):
@@ -55,15 +57,26 @@ def s3(*v):
     return (ctypes.c_int64 * 3)(*v)
 
 
-def fwd(lib, d=64, hq=4, hkv=2, ptr=4096, strides=None, lse=4096):
+def fwd(lib, d=64, hq=4, hkv=2, ptr=4096, strides=None, lse=4096, bf16=False):
     st = strides or s3(4 * 16 * d, 16 * d, d)
-    return lib.fal_fwd(ctypes.c_void_p(ptr), ctypes.c_void_p(ptr), ctypes.c_void_p(ptr), ctypes.c_void_p(ptr),
+    return (lib.fal_fwd_bf16 if bf16 else lib.fal_fwd)(ctypes.c_void_p(ptr), ctypes.c_void_p(ptr), ctypes.c_void_p(ptr), ctypes.c_void_p(ptr),
                        ctypes.c_void_p(lse) if lse else None, 1, hq, hkv, 16, 16, d, st, st, st, st, 0.125, 1, None)
 
 
 def test_forward_rejects_head_dim(lib):
     assert fwd(lib, d=48) == FAL_ERR_UNSUPPORTED
     assert b"head_dim must be 32, 64, 96, 128, or 256, got 48" in lib.fal_last_error()
+
+
+def test_bf16_forward_checks_like_fp16(lib):
+    """The bf16 entry point validates its arguments exactly as the fp16 one does."""
+    for kw, code, msg in ((dict(d=48), FAL_ERR_UNSUPPORTED, b"head_dim must be"),
+                          (dict(hq=6, hkv=4), FAL_ERR_INVALID, b"divisible"),
+                          (dict(ptr=0), FAL_ERR_INVALID, b"null"),
+                          (dict(lse=0), FAL_ERR_INVALID, b"lse")):
+        assert fwd(lib, bf16=True, **kw) == code
+        assert msg in lib.fal_last_error()
+        assert fwd(lib, bf16=False, **kw) == code
 
 
 def test_forward_rejects_gqa_ratio(lib):
