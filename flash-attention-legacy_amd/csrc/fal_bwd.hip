@@ -17,8 +17,8 @@
 //     dK^T += Q^T dS (dO^T and Q^T from the Q/dO tiles via ds_read_b64_tr_b16);
 //     dK/dV stay in registers until the end.
 // * head_dim 256: bwd_pre_kernel (D, zeroed fp32 dQ accumulator), bwd_kernel
-//   (KV-outer, dS^T staged in LDS, dQ = dS K added with fp32 atomics; for head_dim
-//   256 the dK/dV accumulators take two passes of 128 columns) and bwd_post_kernel
+//   (KV-outer, dS^T staged in LDS, dQ = dS K added with fp32 atomics; all 256 dK/dV
+//   columns accumulate in one pass, with K read from its LDS tile) and bwd_post_kernel
 //   (dQ cast to fp16).
 #include <type_traits>
 
@@ -110,6 +110,13 @@ bwd_post_kernel(BwdParams p, int rows, int batched) {
   st_u4((T*)p.dq + dq_off + c, __builtin_bit_cast(u32x4, h));
 }
 
+#ifndef FAL_BWD_KLDS
+#define FAL_BWD_KLDS 1   // head_dim 256: K fragments from the LDS K tile (+20%: no K registers to spill)
+#endif
+#ifndef FAL_BWD_DW
+#define FAL_BWD_DW 256   // head_dim 256: dK/dV columns held per pass (256: one pass, +11% over two passes of 128)
+#endif
+
 // --------------------------------------------------------------------------
 // Main KV-outer kernel
 // --------------------------------------------------------------------------
@@ -121,7 +128,7 @@ bwd_kernel(BwdParams p) {
   static_assert(BMQ == 32, "query tile is one 32-row MFMA block");
   constexpr int BN = NW * 32;
   constexpr int KS = D / 16;
-  constexpr int DW = D > 128 ? 128 : D;   // dK/dV columns accumulated per pass
+  constexpr int DW = D > FAL_BWD_DW ? FAL_BWD_DW : D;   // dK/dV columns accumulated per pass
   constexpr int NPASS = D / DW;
   constexpr int DWB = DW / 32;
   constexpr int DQB = D / 32;
@@ -177,10 +184,12 @@ bwd_kernel(BwdParams p) {
   // K/V rows of this wave (B operands: n = key, k = head dim)
   const int kw0 = n0 + w * 32;
   const int key = kw0 + l32;
-  V8 kreg[KS], vreg[KS];
+  // K of this wave's keys is read from the K tile in LDS (FAL_BWD_KLDS), which leaves
+  // the registers to V and the dK/dV accumulators
+  V8 kreg[FAL_BWD_KLDS ? 1 : KS], vreg[KS];
 #pragma unroll
   for (int t = 0; t < KS; ++t) {
-    kreg[t] = key < nk ? ld8(kbase + (int64_t)key * p.k_ss + t * 16 + hh * 8) : zero8<T>();
+    if (!FAL_BWD_KLDS) kreg[t] = key < nk ? ld8(kbase + (int64_t)key * p.k_ss + t * 16 + hh * 8) : zero8<T>();
     vreg[t] = key < nk ? ld8(vbase + (int64_t)key * p.v_ss + t * 16 + hh * 8) : zero8<T>();
   }
   // K tile, row-major, for dQ = dS K
@@ -267,7 +276,8 @@ bwd_kernel(BwdParams p) {
           f32x16 s = zero_f16(), dp = zero_f16();
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            s = mfma32(ld8(q_s + l32 * LDK + t * 16 + hh * 8), kreg[t], s);
+            s = mfma32(ld8(q_s + l32 * LDK + t * 16 + hh * 8),
+                       FAL_BWD_KLDS ? ld8(ks_s + (w * 32 + l32) * LDK + t * 16 + hh * 8) : kreg[t], s);
             dp = mfma32(ld8(do_s + l32 * LDK + t * 16 + hh * 8), vreg[t], dp);
           }
           // P and dS (element i: query q0 + (i/4)*8 + hh*4 + i%4, key `key`)
