@@ -51,7 +51,8 @@ def patch_llama_attention(model):
                 v = torch.cat([cache[1], v], dim=2)
 
             scale = 1.0 / math.sqrt(head_dim)
-            half = lambda t: t if t.dtype == torch.float16 else t.half()
+            # fp16 and bf16 run natively; other dtypes are cast to fp16
+            half = lambda t: t if t.dtype in (torch.float16, torch.bfloat16) else t.half()
             kv_len = k.shape[2]
             if q_len == 1 and kv_len > 1:
                 # decode: [B, H_q, d] query against the [B, H_kv, S, d] cache
