@@ -11,7 +11,7 @@ against bf16's 8-bit mantissa (one unit in the last place at 1 is 2^-7):
     for their second products; fp16's bound is 1e-2, eight times finer mantissa).
 Coverage: every head dim, causal and not, MHA/GQA/MQA, ragged lengths; varlen
 forward and backward; decode; the autograd function; determinism of the backward;
-a bf16 HF model against eager attention.
+a bf16 HF model against eager attention; C2 (sampled rows) and C3 at full size.
 """
 
 import math
@@ -183,3 +183,42 @@ def test_hf_bf16_model_runs_natively(monkeypatch):
     assert seen and all(dt == torch.bfloat16 for dt in seen)
     cos = torch.nn.functional.cosine_similarity(a.reshape(1, -1), b.reshape(1, -1)).item()
     assert cos > 0.999, cos
+
+
+def test_c2_full_size_sampled_rows():
+    """C2 in bf16 at full size (B=4, 32q/8kv heads, N=4096, d=128, causal): O and L of
+    sampled rows of several heads against exact float64 rows of the same bf16 inputs."""
+    from flash_attn_legacy import hip_ext
+    B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
+    q, k, v = rbf((B, Hq, N, d), 30), rbf((B, Hkv, N, d), 31), rbf((B, Hkv, N, d), 32)
+    scale = 1.0 / math.sqrt(d)
+    o, lse = hip_ext.forward(q, k, v, scale, True)
+    rows = [0, 1, 127, 128, 2047, 4000, N - 1]
+    for bb, h in ((0, 0), (1, 13), (3, 31)):
+        qf, kf, vf = (np64(t) for t in (q[bb, h], k[bb, h // 4], v[bb, h // 4]))
+        ref_o, ref_l = [], []
+        for r in rows:
+            s = kf[: r + 1] @ qf[r] * scale
+            m = s.max()
+            p = np.exp(s - m)
+            ref_o.append(p @ vf[: r + 1] / p.sum())
+            ref_l.append(m + np.log(p.sum()))
+        check_out(o[bb, h, rows], torch.from_numpy(np.stack(ref_o)))
+        assert np.abs(lse[bb, h, rows].double().cpu().numpy() - np.array(ref_l)).max() <= LSE_ATOL
+
+
+def test_c3_full_size_gradients():
+    """C3 in bf16 at full size (B=2, 16 heads, N=2048, d=128, causal): dQ/dK/dV of two
+    heads against the float64 oracle on the same bf16 inputs."""
+    from flash_attn_legacy import hip_ext
+    B, H, N, d = 2, 16, 2048, 128
+    q, k, v, do = (rbf((B, H, N, d), s) for s in (33, 34, 35, 36))
+    scale = 1.0 / math.sqrt(d)
+    o, lse = hip_ext.forward(q, k, v, scale, True)
+    dq, dk, dv = hip_ext.backward(do, q, k, v, o, lse, scale, True)
+    for bb, h in ((0, 0), (1, 9)):
+        sl = lambda t: t[bb:bb + 1, h:h + 1]
+        refs = oracle_bwd(sl(q), sl(k), sl(v), sl(do), scale, True)
+        for name, g, r in zip(("dq", "dk", "dv"), (sl(dq), sl(dk), sl(dv)), refs):
+            e = rel_err(g, r)
+            assert e <= GRAD_RTOL_BF16, f"{name} head {h}: rel err {e:.3e}"
