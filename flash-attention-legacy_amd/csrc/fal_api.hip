@@ -158,6 +158,9 @@ size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
   return align256((size_t)cap * sizeof(int2));
 }
 
+#ifndef FAL_FWD_VARLEN_ORDER
+#define FAL_FWD_VARLEN_ORDER 2   // 2: grouped by sequence; 1: heaviest tile index first over all sequences
+#endif
 static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void* o, float* lse,
                    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs, int64_t total_q,
                    int64_t total_k, int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_q,
@@ -190,8 +193,9 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
   int nb = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
   nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nb, is_causal ? 1 : 0, work,
-                                        cap, st);
+  // grouped by sequence (see varlen_schedule_kernel): K/V locality in each XCD's L2
+  hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nb, FAL_FWD_VARLEN_ORDER,
+                                        work, cap, st);
   if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
 
   FwdParams p{};
