@@ -158,6 +158,9 @@ size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
   return align256((size_t)cap * sizeof(int2));
 }
 
+#ifndef FAL_BWD_DQ_VARLEN_ORDER
+#define FAL_BWD_DQ_VARLEN_ORDER 2
+#endif
 #ifndef FAL_FWD_VARLEN_ORDER
 #define FAL_FWD_VARLEN_ORDER 2   // 2: grouped by sequence; 1: heaviest tile index first over all sequences
 #endif
@@ -443,13 +446,13 @@ static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, c
   if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen schedule");
   dim3 dq_grid(0, 0);
   if (bwd_split_dq((int)head_dim)) {
-    // query tiles for the dQ kernel, longest first when causal
+    // query tiles for the dQ kernel, grouped by sequence (as the forward's list)
     const int bm = bwd_dq_block_m((int)head_dim);
     const int capq = (int)((total_q + bm - 1) / bm + num_seqs);
     int2* qwork = work + align256((size_t)cap * sizeof(int2)) / sizeof(int2);
     int nbq = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
     nbq = nbq < 1 ? 1 : (nbq > 8192 ? 8192 : nbq);
-    e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nbq, is_causal ? 1 : 0, qwork,
+    e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nbq, FAL_BWD_DQ_VARLEN_ORDER, qwork,
                                capq, st);
     if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen dq schedule");
     p.qwork = qwork;
