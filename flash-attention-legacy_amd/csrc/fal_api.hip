@@ -335,7 +335,7 @@ static int fal_bwd_impl(const void* dout, const void* q, const void* k, const vo
   const size_t need = fal_bwd_workspace_size(batch, heads_q, seqlen_q, head_dim);
   if (!workspace || workspace_bytes < need)
     return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
-  if (batch == 0 || seqlen_k == 0 && seqlen_q == 0) return ok();
+  if (batch == 0 || (seqlen_k == 0 && seqlen_q == 0)) return ok();
   const size_t rows = (size_t)batch * heads_q * seqlen_q;
   const size_t acc = bwd_acc_bytes(rows, head_dim);
   p.dq_acc = acc ? static_cast<float*>(workspace) : nullptr;

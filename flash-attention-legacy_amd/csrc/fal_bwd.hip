@@ -38,7 +38,6 @@ template <class T, int D>
 __global__ void __launch_bounds__(256)
 bwd_pre_kernel(BwdParams p, int rows, int batched) {
   using V8 = vec8<T>;
-  using V4 = vec4<T>;
   constexpr int G = row_group<D>();   // lanes per row (power of two; lanes past D idle)
   const int r = blockIdx.x * (256 / G) + threadIdx.x / G;
   const int c = (threadIdx.x % G) * 8;
@@ -81,7 +80,6 @@ template <class T, int D>
 __global__ void __launch_bounds__(256)
 bwd_post_kernel(BwdParams p, int rows, int batched) {
   using V8 = vec8<T>;
-  using V4 = vec4<T>;
   constexpr int G = row_group<D>();
   const int r = blockIdx.x * (256 / G) + threadIdx.x / G;
   const int c = (threadIdx.x % G) * 8;
@@ -637,7 +635,7 @@ bwd2_kernel(BwdParams p) {
           V8 od = ld8(do_s + faddr(0)), ov = ld8(vw_s + faddr(0));
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            V8 nq, nk, nd, nv;
+            V8 nq = oq, nk = ok, nd = od, nv = ov;   // (unused after the last step)
             if (t + 1 < KS) {
               const int fa = faddr(t + 1);
               nq = ld8(q_s + fa);
@@ -691,7 +689,7 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
             for (int st = 0; st < 2 * DWB; ++st) {
               const int ks = st / DWB, db = st % DWB;
-              V8 no, nq;
+              V8 no = ao, nq = aq;   // (unused after the last step)
               if (st + 1 < 2 * DWB) {
                 no = trk(do_s, (st + 1) % DWB, (st + 1) / DWB * 16);
                 nq = trk(q_s, (st + 1) % DWB, (st + 1) / DWB * 16);
