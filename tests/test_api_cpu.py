@@ -114,3 +114,15 @@ def test_utils_without_gpu():
     assert check_gpu_compatibility(verbose=False) is False
     with pytest.raises(RuntimeError):
         get_device_info()
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message instead of running."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.join(os.path.dirname(__file__), "..")
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
