@@ -11,7 +11,8 @@ against bf16's 8-bit mantissa (one unit in the last place at 1 is 2^-7):
     for their second products; fp16's bound is 1e-2, eight times finer mantissa).
 Coverage: every head dim, causal and not, MHA/GQA/MQA, ragged lengths; varlen
 forward and backward; decode; the autograd function; determinism of the backward;
-a bf16 HF model against eager attention; C2 (sampled rows) and C3 at full size.
+a bf16 HF model against eager attention (also with a padded batch); the attention
+module; C2 (sampled rows) and C3 at full size.
 """
 
 import math
@@ -222,3 +223,55 @@ def test_c3_full_size_gradients():
         for name, g, r in zip(("dq", "dk", "dv"), (sl(dq), sl(dk), sl(dv)), refs):
             e = rel_err(g, r)
             assert e <= GRAD_RTOL_BF16, f"{name} head {h}: rel err {e:.3e}"
+
+
+def test_module_bf16_forward_backward():
+    """FlashMultiHeadAttention in bf16 runs the bf16 kernels (no cast to fp16): output and
+    input gradient against an fp32 copy of the module with fp32 attention."""
+    import torch.nn.functional as F
+    from flash_attn_legacy import FlashMultiHeadAttention
+    from oracle.torch_ref import ref_attention
+    torch.manual_seed(0)
+    m = FlashMultiHeadAttention(512, num_heads=8, num_kv_heads=2, causal=True).cuda().to(torch.bfloat16)
+    x = rbf((2, 64, 512), 40).requires_grad_(True)
+    out = m(x)
+    assert out.dtype == torch.bfloat16
+    g = rbf((2, 64, 512), 41, 0.1)
+    out.backward(g)
+    p = {n: t.detach().float().cpu() for n, t in m.named_parameters()}
+    xf = x.detach().float().cpu().requires_grad_(True)
+    q = F.linear(xf, p["q_proj.weight"], p["q_proj.bias"]).view(2, 64, 8, 64).transpose(1, 2)
+    k = F.linear(xf, p["k_proj.weight"], p["k_proj.bias"]).view(2, 64, 2, 64).transpose(1, 2)
+    v = F.linear(xf, p["v_proj.weight"], p["v_proj.bias"]).view(2, 64, 2, 64).transpose(1, 2)
+    o = ref_attention(q, k, v, m.scale, True).transpose(1, 2).reshape(2, 64, 512)
+    ref = F.linear(o, p["out_proj.weight"], p["out_proj.bias"])
+    ref.backward(g.float().cpu())
+    cos = lambda a, b: F.cosine_similarity(a.float().cpu().reshape(1, -1), b.reshape(1, -1)).item()
+    assert cos(out.detach(), ref.detach()) > 0.999
+    assert cos(x.grad, xf.grad) > 0.99
+
+
+def test_hf_bf16_padded_batch():
+    """A bf16 LLaMA with a left-padded batch: the padded prefill runs the bf16 varlen
+    kernel; logits of real tokens match eager attention's."""
+    import flash_attn_legacy  # noqa: F401
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    def model(impl):
+        cfg = LlamaConfig(vocab_size=256, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                          num_attention_heads=8, num_key_value_heads=2, max_position_embeddings=512)
+        cfg._attn_implementation = impl
+        torch.manual_seed(0)
+        return LlamaForCausalLM(cfg).cuda().to(torch.bfloat16).eval()
+
+    flash, eager = model("flash_attn_legacy"), model("eager")
+    eager.load_state_dict(flash.state_dict())
+    ids = torch.randint(0, 256, (2, 80), device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    mask = torch.ones_like(ids)
+    mask[0, :25] = 0
+    with torch.no_grad():
+        a = flash(ids, attention_mask=mask).logits.float()
+        b = eager(ids, attention_mask=mask).logits.float()
+    real = mask.bool()
+    cos = torch.nn.functional.cosine_similarity(a[real].reshape(1, -1), b[real].reshape(1, -1)).item()
+    assert torch.isfinite(a[real]).all() and cos > 0.999, cos
