@@ -158,6 +158,9 @@ size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
   return align256((size_t)cap * sizeof(int2));
 }
 
+#ifndef FAL_BWD_VARLEN_ORDER
+#define FAL_BWD_VARLEN_ORDER 3   // KV-outer list: 3 grouped by sequence, 0 by tile index over all sequences
+#endif
 #ifndef FAL_BWD_DQ_VARLEN_ORDER
 #define FAL_BWD_DQ_VARLEN_ORDER 2
 #endif
@@ -442,7 +445,9 @@ static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, c
   // Every key row of every segment is covered by exactly one work item, which writes
   // its dK/dV rows (zeros when the segment has no query rows).  Rows outside all
   // segments are not written; the caller pre-zeroes dk/dv if it needs them defined.
-  hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, (int)total_k, bn, nb, 0, work, cap, st);
+  // key tiles grouped by sequence, the tile with the most query rows first
+  hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, (int)total_k, bn, nb, FAL_BWD_VARLEN_ORDER,
+                                        work, cap, st);
   if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen schedule");
   dim3 dq_grid(0, 0);
   if (bwd_split_dq((int)head_dim)) {
@@ -462,7 +467,8 @@ static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, c
     if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
     dq_grid = dim3((unsigned)nblocks);
   }
-  return run_bwd(p, (int)head_dim, is_causal != 0, dim3(cap, (unsigned)heads_kv), dq_grid, false, st);
+  if ((int64_t)cap * heads_kv > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
+  return run_bwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)(cap * heads_kv)), dq_grid, false, st);
 }
 int fal_bwd_varlen(const void* dout, const void* q, const void* k, const void* v, const void* o, const float* lse,
                    void* dq, void* dk, void* dv, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,

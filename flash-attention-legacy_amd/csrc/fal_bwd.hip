@@ -151,9 +151,12 @@ bwd_kernel(BwdParams p) {
 
   int b, hkv, kt, q_off, k_off, nq, nk;
   if (p.cu_q) {
-    const int2 wk = p.work[blockIdx.x];
+    // 1-D grid, KV head fastest: block i runs on XCD i % 8, so for a multiple of 8 KV
+    // heads each XCD walks one KV head's items in list order (grouped by sequence) and
+    // the query tiles they all read stay in its L2
+    const int2 wk = p.work[blockIdx.x / p.Hkv];
     if (wk.x < 0) return;
-    hkv = blockIdx.y;
+    hkv = blockIdx.x % p.Hkv;
     b = 0;
     kt = wk.y;
     seg_bounds(p.cu_q, wk.x, p.total_q, q_off, nq);
@@ -441,9 +444,12 @@ bwd2_kernel(BwdParams p) {
   // ---- work item: up to two key tiles of one (batch, KV head) ----
   int b, hkv, q_off, k_off, nq, nk, kt_a, kt_b;
   if (p.cu_q) {
-    const int2 wk = p.work[blockIdx.x];
+    // 1-D grid, KV head fastest: block i runs on XCD i % 8, so for a multiple of 8 KV
+    // heads each XCD walks one KV head's items in list order (grouped by sequence) and
+    // the query tiles they all read stay in its L2
+    const int2 wk = p.work[blockIdx.x / p.Hkv];
     if (wk.x < 0) return;
-    hkv = blockIdx.y;
+    hkv = blockIdx.x % p.Hkv;
     b = 0;
     kt_a = wk.y;
     kt_b = -1;

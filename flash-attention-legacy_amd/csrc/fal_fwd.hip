@@ -416,10 +416,11 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
   int* cur = sh + nbuckets;
   for (int i = threadIdx.x; i < nbuckets; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  if (descending == 2) {
+  if (descending >= 2) {
     // Grouped by sequence: longest sequences first (bucketed by tile count), each
-    // sequence's tiles contiguous, heaviest (last) tile first.  The workgroups an XCD
-    // runs at once then share one or two sequences' K/V in its L2.
+    // sequence's tiles contiguous; 2: last tile first (query-outer causal work grows
+    // with the tile index), 3: first tile first (KV-outer causal work shrinks with it).
+    // The workgroups an XCD runs at once then share one or two sequences' data in L2.
     for (int s = threadIdx.x; s < num_seqs; s += blockDim.x) {
       int off, len;
       seg_bounds(cu, s, rows, off, len);
@@ -444,7 +445,7 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
       if (nt == 0) continue;
       const int pos = atomicAdd(&cur[min(nt - 1, nbuckets - 1)], nt);
       for (int t = 0; t < nt; ++t)
-        if (pos + t < capacity) work[pos + t] = make_int2(s, nt - 1 - t);
+        if (pos + t < capacity) work[pos + t] = make_int2(s, descending == 2 ? nt - 1 - t : t);
     }
     for (int i = total + threadIdx.x; i < capacity; i += blockDim.x) work[i] = make_int2(-1, -1);
     return;
