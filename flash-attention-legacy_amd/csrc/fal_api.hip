@@ -443,11 +443,14 @@ static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, c
   int nb = cdiv((int)(max_seqlen_k > 0 ? max_seqlen_k : 1), bn);
   nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
   // Every key row of every segment is covered by exactly one work item, which writes
-  // its dK/dV rows (zeros when the segment has no query rows).  Rows outside all
-  // segments are not written; the caller pre-zeroes dk/dv if it needs them defined.
+  // its dK/dV rows (zeros when the segment has no query rows).  The schedule kernel
+  // writes zeros to the rows outside all segments (dK/dV here; dQ in the query-tile
+  // schedule below, or the d 256 accumulator, zeroed for every row).
   // key tiles grouped by sequence, the tile with the most query rows first
+  const ZeroRows zkv{dk, dv, dk_strides[2], dk_strides[1], dv_strides[2], dv_strides[1], (int)heads_kv,
+                     (int)head_dim};
   hipError_t e = launch_varlen_schedule(cu_seqlens_k, (int)num_seqs, (int)total_k, bn, nb, FAL_BWD_VARLEN_ORDER,
-                                        work, cap, st);
+                                        work, cap, st, &zkv);
   if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen schedule");
   dim3 dq_grid(0, 0);
   if (bwd_split_dq((int)head_dim)) {
@@ -457,8 +460,9 @@ static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, c
     int2* qwork = work + align256((size_t)cap * sizeof(int2)) / sizeof(int2);
     int nbq = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
     nbq = nbq < 1 ? 1 : (nbq > 8192 ? 8192 : nbq);
+    const ZeroRows zq{dq, nullptr, dq_strides[2], dq_strides[1], 0, 0, (int)heads_q, (int)head_dim};
     e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nbq, FAL_BWD_DQ_VARLEN_ORDER, qwork,
-                               capq, st);
+                               capq, st, &zq);
     if (e != hipSuccess) return launch_status(e, "fal_bwd_varlen dq schedule");
     p.qwork = qwork;
     p.n_qitems = capq;

@@ -108,6 +108,9 @@ bwd_post_kernel(BwdParams p, int rows, int batched) {
   st_u4((T*)p.dq + dq_off + c, __builtin_bit_cast(u32x4, h));
 }
 
+#ifndef FAL_PRESCALE_FP16
+#define FAL_PRESCALE_FP16 0
+#endif
 #ifndef FAL_BWD_KLDS
 #define FAL_BWD_KLDS 1   // head_dim 256: K fragments from the LDS K tile (+20%: no K registers to spill)
 #endif
@@ -388,9 +391,8 @@ bwd_kernel(BwdParams p) {
 // S = Q K^T and dP = dO V^T for its 32 keys x 32 rows, P = exp2(S - L*log2e),
 // dS = P (dP - D), then dV^T += dO^T P and dK^T += Q^T dS in registers (Q^T, dO^T
 // read transposed from LDS, P and dS taken from the accumulators as B operands).
-//   - K is scaled by scale*log2e once per key tile, in LDS, and the S accumulator
-//     starts at -L*log2e, the dP accumulator at -D: the MFMAs produce the exponent
-//     and dP - D directly.
+//   - The dP accumulator starts at -D, so the MFMAs produce dP - D directly; the
+//     exponent of P is one FMA, S*scale*log2e - L*log2e.
 //   - Operands of MFMA step t+1 are read before the MFMAs of step t.
 //   - Only tiles that straddle the diagonal apply the causal mask.
 //   - MFMA phases run at raised wave priority, so a SIMD's other wave fills their
@@ -408,10 +410,11 @@ __global__ void __launch_bounds__(FAL_BWD2_NW * 64) __attribute__((amdgpu_waves_
 bwd2_kernel(BwdParams p) {
   using V8 = vec8<T>;
   using V4 = vec4<T>;
-  // fp16: the K tile is pre-multiplied by scale*log2(e) in LDS and the S accumulator
-  // starts at -L*log2e; bf16 keeps K exact (8-bit mantissa) and applies both to the
-  // fp32 scores with one FMA each
-  constexpr bool PRESCALE = std::is_same<T, half_t>::value;
+  // K stays exact and scale*log2(e) and -L*log2e are applied to the fp32 scores with
+  // one FMA each.  FAL_PRESCALE_FP16 instead pre-multiplies an fp16 K tile in LDS
+  // (rounded once) and starts the S accumulator at -L*log2e; that rounding costs
+  // accuracy at large logits, so it is off.
+  constexpr bool PRESCALE = FAL_PRESCALE_FP16 && std::is_same<T, half_t>::value;
   using TL = SwizzledTile<D>;
   constexpr int NW = FAL_BWD2_NW, BN = NW * 16, BMQ = 64;
   constexpr int NKG = NW / 2;             // key groups of 32 (x 2 query halves)
@@ -546,8 +549,8 @@ bwd2_kernel(BwdParams p) {
       dk_acc[i] = zero_f16();
       dv_acc[i] = zero_f16();
     }
-    // K tile *= scale*log2e (in fp32, rounded once to fp16), so that S comes out of
-    // the MFMAs already in log2 units and the S accumulator can start at -L*log2e
+    // (FAL_PRESCALE_FP16 only) K tile *= scale*log2e, rounded once to fp16, so that S
+    // comes out of the MFMAs in log2 units and its accumulator can start at -L*log2e
     wait_vmcnt0();
     __syncthreads();
 #pragma unroll

@@ -7,15 +7,15 @@
 // valid key gives O = 0 and L = -inf.
 //
 // Work decomposition (one workgroup = NW waves = 32*NW*RB query rows of one head):
-// * each wave owns 32 query rows (RB = 1); its Q slice, pre-multiplied by
-//   scale*log2(e), stays in VGPRs for the whole kernel as the B operand of
+// * each wave owns 32 query rows (RB = 1); its Q slice stays in VGPRs for the
+//   whole kernel as the B operand of
 //   S^T = K Q^T, so the accumulator puts one query row per lane (two lanes per row,
 //   one per wave half) and row reductions are in-lane plus one permlane32 swap;
 // * K/V tiles of BN keys are copied HBM -> LDS by buffer loads that bypass VGPRs,
 //   into XOR-swizzled, double-buffered tiles (conflict-free row and transposed
 //   reads); one buffer resource per tile zero-fills rows past the sequence end;
-// * the S^T accumulators start at -m (the row's reference max), so the MFMAs give
-//   the exponent of P directly; the row max is recomputed only when a tile's P
+// * one FMA per score gives the exponent s*scale*log2(e) - m of P, m being the row's
+//   reference max; the row max is recomputed only when a tile's P
 //   could leave fp16 range (its per-lane p sum exceeds 2^15) or on a row's first tile;
 // * P^T goes straight from the S^T accumulator into the B operand of O^T = V^T P^T;
 //   V^T comes from the row-major V tile through ds_read_b64_tr_b16;
@@ -34,6 +34,9 @@ namespace fal {
 #endif
 #ifndef FAL_FWD_BN
 #define FAL_FWD_BN 64
+#endif
+#ifndef FAL_PRESCALE_FP16
+#define FAL_PRESCALE_FP16 0
 #endif
 #ifndef FAL_FWD_KDEPTH
 #define FAL_FWD_KDEPTH 2
@@ -95,9 +98,10 @@ fwd_kernel(FwdParams p) {
   using TL = SwizzledTile<D>;
   using V8 = vec8<T>;
   using V4 = vec4<T>;
-  // fp16: Q is pre-multiplied by scale*log2(e) and rounded once (11-bit mantissa);
-  // bf16 keeps Q exact and scales the fp32 scores instead (one FMA per score)
-  constexpr bool PRESCALE = std::is_same<T, half_t>::value;
+  // Q stays exact and the fp32 scores are scaled (one FMA per score).  FAL_PRESCALE_FP16
+  // instead pre-multiplies an fp16 Q by scale*log2(e), rounded once to fp16: that saves
+  // the FMA but shifts large scores by up to ~1e-2 in log2 units, so it is off.
+  constexpr bool PRESCALE = FAL_PRESCALE_FP16 && std::is_same<T, half_t>::value;
   constexpr int BM = NW * 32 * RB;  // query rows per workgroup (RB 32-row blocks per wave)
   constexpr int KS = D / 16;        // MFMA k-steps over the head dim
   constexpr int NKB = BN / 32;      // 32-key blocks per tile
@@ -131,8 +135,8 @@ fwd_kernel(FwdParams p) {
 
   // ---- Q slices of this wave into registers (B operand: n = query row, k = head dim) ----
   // Row block rb of wave w covers rows m0 + (w*RB + rb)*32 ..; each K or V fragment read
-  // from LDS feeds RB MFMAs.  Q is pre-multiplied by c = softmax_scale * log2(e) (the
-  // sign included), so the MFMA yields scores in the log2 domain directly.
+  // from LDS feeds RB MFMAs.  c = softmax_scale * log2(e), the sign included, takes
+  // the scores to the log2 domain.
   const float c = p.scale_log2;
   int row[RB];
   V8 qreg[RB][KS];
@@ -212,8 +216,8 @@ fwd_kernel(FwdParams p) {
     for (int i = 0; i < DB; ++i) oacc[rb][i] = zero_f16();
   // m_run: reference max of the row (log2 domain); it may lag the true running max, as
   // long as every p = exp2(s - m_run) of a tile fits fp16 (the tile's p sum <= 2^15).
-  // negm: -m_run broadcast over an accumulator block, the starting value of S^T, so the
-  // MFMAs produce s - m_run without a VALU pass.
+  // negm: -m_run broadcast over an accumulator block (the addend of the score FMA, or
+  // the starting value of S^T under FAL_PRESCALE_FP16).
   float m_run[RB], l_run[RB];
   f32x16 negm[RB];
 #pragma unroll
@@ -410,12 +414,42 @@ fwd_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
 varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int tile, int nbuckets,
-                       int descending, int2* __restrict__ work, int capacity) {
+                       int descending, int2* __restrict__ work, int capacity, ZeroRows zero) {
   extern __shared__ int sh[];            // [nbuckets] counts, then [nbuckets] cursors
   int* cnt = sh;
   int* cur = sh + nbuckets;
+  __shared__ int seg_end;
   for (int i = threadIdx.x; i < nbuckets; i += blockDim.x) cnt[i] = 0;
+  if (threadIdx.x == 0) seg_end = 0;
   __syncthreads();
+  if (zero.a) {
+    // rows [0, start of segment 0) and [end of the last segment, rows) are in no segment
+    // (for a monotone cu_seqlens): write zeros there, as the reference's per-sequence
+    // backward leaves them (zeros_like, flash_attn.py:125-131)
+    for (int s = threadIdx.x; s < num_seqs; s += blockDim.x) {
+      int off, len;
+      seg_bounds(cu, s, rows, off, len);
+      atomicMax(&seg_end, off + len);
+    }
+    __syncthreads();
+    int first = rows, flen = 0;
+    if (num_seqs > 0) seg_bounds(cu, 0, rows, first, flen);
+    const int last = seg_end;
+    const int cpr = zero.heads * (zero.d / 8);   // 16-byte chunks per row
+    const int nlo = first, nhi = rows - max(last, first);
+    const int64_t nchunks = (int64_t)(nlo + nhi) * cpr;
+    for (int64_t i = threadIdx.x; i < nchunks; i += blockDim.x) {
+      const int rr = (int)(i / cpr);
+      const int r = rr < nlo ? rr : max(last, first) + (rr - nlo);
+      const int ch = (int)(i % cpr);
+      const int h = ch / (zero.d / 8), c8 = (ch % (zero.d / 8)) * 8;
+      st_u4(static_cast<half_t*>(zero.a) + (int64_t)r * zero.a_row + (int64_t)h * zero.a_head + c8,
+            u32x4{0, 0, 0, 0});
+      if (zero.b)
+        st_u4(static_cast<half_t*>(zero.b) + (int64_t)r * zero.b_row + (int64_t)h * zero.b_head + c8,
+              u32x4{0, 0, 0, 0});
+    }
+  }
   if (descending >= 2) {
     // Grouped by sequence: longest sequences first (bucketed by tile count), each
     // sequence's tiles contiguous; 2: last tile first (query-outer causal work grows
@@ -547,10 +581,12 @@ hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStrea
 }
 
 hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int rows, int tile, int nbuckets, int descending,
-                                  int2* work, int capacity, hipStream_t st) {
+                                  int2* work, int capacity, hipStream_t st, const ZeroRows* zero) {
   const size_t shmem = 2 * sizeof(int) * (size_t)nbuckets;
+  ZeroRows z{};
+  if (zero) z = *zero;
   hipLaunchKernelGGL(varlen_schedule_kernel, dim3(1), dim3(1024), shmem, st, cu, num_seqs, rows, tile,
-                     nbuckets, descending, work, capacity);
+                     nbuckets, descending, work, capacity, z);
   return hipGetLastError();
 }
 

@@ -98,8 +98,17 @@ struct DecodeParams {
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 int fwd_block_m(int d);
+// Rows of up to two packed [rows, heads, d] 16-bit tensors that the schedule kernel
+// zeroes: those before the first segment and from the end of the last one on
+// (the rows no segment covers when cu_seqlens is monotone).
+struct ZeroRows {
+  void* a;
+  void* b;                            // optional
+  int64_t a_row, a_head, b_row, b_head;   // element strides
+  int heads, d;
+};
 hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int rows, int tile, int nbuckets, int descending,
-                                  int2* work, int capacity, hipStream_t st);
+                                  int2* work, int capacity, hipStream_t st, const ZeroRows* zero = nullptr);
 
 int bwd_block_n(int d);
 hipError_t launch_bwd(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st);

@@ -165,6 +165,14 @@ def _check_half_cuda(name: str, t: torch.Tensor, dtype: Optional[torch.dtype] = 
         raise RuntimeError(f"{name} must be {str(dtype)[6:]} like Q")
 
 
+def _check_lse(L: torch.Tensor, shape, device) -> None:
+    """L is the forward's fp32 log-sum-exp of `shape` on `device` (the kernels index it
+    by the problem's sizes, so a smaller tensor would be read out of bounds)."""
+    if L.dtype != torch.float32 or tuple(L.shape) != tuple(shape) or L.device != device:
+        raise RuntimeError(f"L must be float32 {list(shape)} on {device}, got {L.dtype} "
+                           f"{list(L.shape)} on {L.device}")
+
+
 def _fn(name: str, dtype: torch.dtype):
     """The library entry point for an element type (fp16, or its _bf16 form)."""
     return getattr(_lib, name + "_bf16") if dtype == torch.bfloat16 else getattr(_lib, name)
@@ -248,6 +256,8 @@ def backward(dO, Q, K, V, O, L, softmax_scale: float, is_causal: bool = False) -
     (csrc/flash_attn_legacy.cpp:115-120); dQ has Q's shape, dK/dV have K/V's."""
     if not (Q.is_cuda and Q.dtype in DTYPES):
         raise RuntimeError("Q must be CUDA float16 or bfloat16")
+    if Q.dim() != 4 or K.dim() != 4:
+        raise RuntimeError("Q, K must be 4D")
     if dO.shape != Q.shape:
         raise RuntimeError("dO shape must match Q")
     B, Hq, N, d = Q.shape
@@ -256,6 +266,13 @@ def backward(dO, Q, K, V, O, L, softmax_scale: float, is_causal: bool = False) -
         raise RuntimeError("H_q must be divisible by H_kv for GQA")
     for name, t in (("dO", dO), ("K", K), ("V", V), ("O", O)):
         _check_half_cuda(name, t, Q.dtype)
+    if K.shape[0] != B or K.shape[3] != d:
+        raise RuntimeError("K shape mismatch")
+    if V.shape != K.shape:
+        raise RuntimeError("V shape must match K")
+    if O.shape != Q.shape:
+        raise RuntimeError("O shape must match Q")
+    _check_lse(L, (B, Hq, N), Q.device)
     dO, Q, K, V, O = (_usable(t) for t in (dO, Q, K, V, O))
     L = L.contiguous()
     dQ = torch.empty((B, Hq, N, d), dtype=Q.dtype, device=Q.device)
@@ -285,18 +302,37 @@ def backward_varlen(dO, Q, K, V, O, L, cu_seqlens_q, cu_seqlens_k, max_seqlen_q:
         raise RuntimeError("Q must be CUDA float16 or bfloat16")
     for name, t in (("dO", dO), ("K", K), ("V", V), ("O", O)):
         _check_half_cuda(name, t, Q.dtype)
+    if Q.dim() != 3 or K.dim() != 3:
+        raise RuntimeError("Q, K must be 3D")
     if dO.shape != Q.shape:
         raise RuntimeError("dO shape must match Q")
     total_q, Hq, d = Q.shape
     total_k, Hkv = K.shape[0], K.shape[1]
+    if Hq % Hkv != 0:
+        raise RuntimeError("H_q must be divisible by H_kv for GQA")
+    if K.shape[2] != d:
+        raise RuntimeError("K,V head_dim mismatch")
+    if V.shape != K.shape:
+        raise RuntimeError("V shape must match K")
+    if O.shape != Q.shape:
+        raise RuntimeError("O shape must match Q")
+    _check_lse(L, (total_q, Hq), Q.device)
+    if cu_seqlens_q.dim() != 1 or cu_seqlens_q.shape[0] < 1:
+        raise RuntimeError("cu_seqlens_q must be a 1-D tensor of num_seqs + 1 offsets")
     num_seqs = cu_seqlens_q.shape[0] - 1
+    if tuple(cu_seqlens_k.shape) != (num_seqs + 1,):
+        raise RuntimeError("cu_seqlens_k length mismatch")
+    for name, cu in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
+        if cu.dtype != torch.int32:
+            raise RuntimeError(f"{name} must be int32")
     dO, Q, K, V, O = (_usable(t) for t in (dO, Q, K, V, O))
     L = L.contiguous()
-    cu_q = cu_seqlens_q.to(device=Q.device, dtype=torch.int32).contiguous()
-    cu_k = cu_seqlens_k.to(device=Q.device, dtype=torch.int32).contiguous()
+    cu_q = cu_seqlens_q.to(Q.device).contiguous()
+    cu_k = cu_seqlens_k.to(Q.device).contiguous()
+    # rows outside every segment come back zero (written by the library's schedule kernels)
     dQ = torch.empty((total_q, Hq, d), dtype=Q.dtype, device=Q.device)
-    dK = torch.zeros((total_k, Hkv, d), dtype=Q.dtype, device=Q.device)
-    dV = torch.zeros((total_k, Hkv, d), dtype=Q.dtype, device=Q.device)
+    dK = torch.empty((total_k, Hkv, d), dtype=Q.dtype, device=Q.device)
+    dV = torch.empty((total_k, Hkv, d), dtype=Q.dtype, device=Q.device)
     ws = _workspace(_lib.fal_bwd_varlen_workspace_size(num_seqs, total_q, total_k, Hq, d), Q.device)
     st = lambda t: _strides(t, (None, 1, 0))
     with torch.cuda.device(Q.device):
@@ -330,8 +366,12 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_
         raise RuntimeError(f"unknown cache_layout {cache_layout!r}")
     if k_cache.shape != v_cache.shape or k_cache.shape[0] != B or k_cache.shape[3] != d:
         raise RuntimeError("k_cache / v_cache shape mismatch")
+    if cache_seqlens.numel() != B:
+        raise RuntimeError(f"cache_seqlens must hold {B} lengths, got {cache_seqlens.numel()}")
+    if mask_bias is not None and (mask_bias.dim() != 2 or mask_bias.shape[0] != B or mask_bias.shape[1] < S):
+        raise RuntimeError(f"mask_bias must be [B={B}, >= S={S}], got {tuple(mask_bias.shape)}")
     q, k_cache, v_cache = _usable(q), _usable(k_cache), _usable(v_cache)
-    seqlens = cache_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    seqlens = cache_seqlens.reshape(-1).to(device=q.device, dtype=torch.int32).contiguous()
     bias = None
     if mask_bias is not None:
         bias = mask_bias.to(device=q.device, dtype=torch.float32)

@@ -1,71 +1,129 @@
-"""
-GPU detection, compatibility checking and a quick benchmark (reference utils.py),
-for AMD Instinct GPUs.  The kernels are built for gfx950 (MI350 / MI355X, CDNA4).
+"""Device detection, compatibility report and a flash-vs-standard benchmark for
+AMD Instinct GPUs.
+
+The public names and arguments are those of the reference's ``utils.py``
+(``get_device_info``, ``check_gpu_compatibility``, ``benchmark_flash_vs_standard``,
+flash_attn_legacy/utils.py:16-125).  What decides support here is the library
+itself: ``fal_device_supported`` reports whether ``libfal_hip.so`` holds code for
+the device (gfx950, MI350X / MI355X).  The benchmark reports absolute rates and
+the fraction of the device's dense fp16 MFMA peak next to the timings.
 """
 
-from typing import Dict, Optional
+from __future__ import annotations
+
+import math
+from typing import Callable, Dict, Optional
 
 import torch
 
-_GFX_TO_ARCH = {
-    "gfx950": "CDNA4 (MI350X / MI355X)",
-    "gfx942": "CDNA3 (MI300X / MI325X)",
-    "gfx90a": "CDNA2 (MI200)",
+# gfx target -> (family, products)
+_TARGETS = {
+    "gfx950": ("CDNA4", "MI350X / MI355X"),
+    "gfx942": ("CDNA3", "MI300X / MI325X"),
+    "gfx90a": ("CDNA2", "MI200"),
+    "gfx908": ("CDNA1", "MI100"),
 }
 
+# Published per-device peaks of the supported target: dense fp16 MFMA (TFLOP/s) and HBM (GB/s)
+_PEAKS = {"gfx950": (2500.0, 8000.0)}
 
-def _gfx(props) -> str:
-    return getattr(props, "gcnArchName", "").split(":")[0]
+
+def _target(props) -> str:
+    """'gfx950' from a gcnArchName such as 'gfx950:sramecc+:xnack-'."""
+    return (getattr(props, "gcnArchName", "") or "").split(":", 1)[0]
+
+
+def _library_supports(index: int) -> bool:
+    try:
+        from . import hip_ext
+    except ImportError:
+        return False
+    return hip_ext.device_supported(index)
 
 
 def get_device_info(device: Optional[int] = None) -> Dict:
-    """Detailed GPU information.  Keys of the reference (utils.py:16-45) are kept;
-    ``sm_version`` is major*10+minor of the HIP device (95 on gfx950)."""
+    """Properties of a GPU and whether this library runs on it.
+
+    Keys shared with the reference: name, sm_version (HIP's major*10 + minor, 95 on
+    gfx950), arch, total_memory_gb, shared_mem_per_block, multiprocessor_count,
+    has_tensor_cores (MFMA matrix cores), kernel_path, supported.  Added: gfx_arch,
+    peak_fp16_tflops and peak_hbm_gbs (None for an unsupported target).
+    Raises RuntimeError without a GPU, like the reference."""
     if not torch.cuda.is_available():
         raise RuntimeError("CUDA not available")
-    if device is None:
-        device = torch.cuda.current_device()
-
-    props = torch.cuda.get_device_properties(device)
-    sm = props.major * 10 + props.minor
-    gfx = _gfx(props)
-    supported = gfx == "gfx950"
+    index = torch.cuda.current_device() if device is None else int(device)
+    props = torch.cuda.get_device_properties(index)
+    gfx = _target(props)
+    family, products = _TARGETS.get(gfx, ("unknown", gfx or "unknown target"))
+    supported = _library_supports(index)
+    peak_flops, peak_hbm = _PEAKS.get(gfx, (None, None))
     return {
         "name": props.name,
-        "sm_version": sm,
+        "sm_version": props.major * 10 + props.minor,
         "gfx_arch": gfx,
-        "arch": _GFX_TO_ARCH.get(gfx, f"Unknown ({gfx or 'SM ' + str(sm)})"),
-        "total_memory_gb": round(props.total_memory / (1024 ** 3), 2),
-        "shared_mem_per_block": getattr(props, "max_shared_memory_per_block",
-                                        getattr(props, "shared_memory_per_block", 0)),
+        "arch": f"{family} ({products})",
+        "total_memory_gb": round(props.total_memory / 2 ** 30, 2),
+        "shared_mem_per_block": int(getattr(props, "shared_memory_per_block",
+                                            getattr(props, "max_shared_memory_per_block", 0))),
         "multiprocessor_count": props.multi_processor_count,
-        "has_tensor_cores": supported,   # MFMA matrix cores
-        "kernel_path": "gfx950 path: MFMA 32x32x16 fp16" if supported else "Unsupported (gfx950 required)",
+        "has_tensor_cores": family in ("CDNA2", "CDNA3", "CDNA4"),
+        "kernel_path": ("gfx950 HIP kernels: fp16/bf16 MFMA, LDS-staged K/V, split-K decode"
+                        if supported else f"none: libfal_hip.so has no code for {gfx or 'this device'}"),
+        "peak_fp16_tflops": peak_flops,
+        "peak_hbm_gbs": peak_hbm,
         "supported": supported,
     }
 
 
 def check_gpu_compatibility(device: Optional[int] = None, verbose: bool = True) -> bool:
-    """Check if the current GPU runs flash_attn_legacy (reference utils.py:48-68)."""
+    """True if flash_attn_legacy's kernels run on the GPU; with verbose, print a report."""
     if not torch.cuda.is_available():
         if verbose:
-            print("CUDA is not available")
+            print("No GPU visible to PyTorch (torch.cuda.is_available() is False)")
         return False
-
     info = get_device_info(device)
     if verbose:
-        print(f"GPU: {info['name']}")
-        print(f"Architecture: {info['arch']} ({info['gfx_arch']})")
-        print(f"Memory: {info['total_memory_gb']} GB")
-        print(f"CUs: {info['multiprocessor_count']}")
-        print(f"Matrix cores: {'yes' if info['has_tensor_cores'] else 'no'}")
-        print(f"Shared Mem/Block: {info['shared_mem_per_block']} bytes")
-        print(f"Kernel path: {info['kernel_path']}")
-        if info["supported"]:
-            print(f"\n[OK] {info['name']} is supported")
-        else:
-            print(f"\n[FAIL] {info['gfx_arch']} not supported (need gfx950)")
-    return info["supported"]
+        rows = [
+            ("device", info["name"]),
+            ("target", f"{info['gfx_arch']} - {info['arch']}"),
+            ("compute units", info["multiprocessor_count"]),
+            ("memory", f"{info['total_memory_gb']} GiB"),
+            ("LDS per workgroup", f"{info['shared_mem_per_block']} bytes"),
+            ("kernels", info["kernel_path"]),
+        ]
+        width = max(len(k) for k, _ in rows)
+        for k, val in rows:
+            print(f"{k:<{width}} : {val}")
+        print("supported" if info["supported"] else "NOT supported (needs gfx950)")
+    return bool(info["supported"])
+
+
+def _event_ms(fn: Callable[[], object], warmup: int, iters: int) -> float:
+    """Mean milliseconds of fn() over `iters` back-to-back calls, from HIP events on the
+    current stream (the stream both implementations launch on)."""
+    for _ in range(max(warmup, 0)):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def _peak_mb(fn: Callable[[], object]) -> float:
+    """Device memory (MB) one call needs beyond what is already allocated: its
+    outputs plus its temporaries at their high-water mark."""
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    out = fn()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    del out
+    return peak / 1e6
 
 
 def benchmark_flash_vs_standard(
@@ -73,50 +131,51 @@ def benchmark_flash_vs_standard(
     head_dim: int = 64, is_causal: bool = False,
     num_warmup: int = 10, num_iters: int = 100
 ) -> Dict:
-    """Benchmark Flash Attention vs standard PyTorch attention (reference utils.py:71-125)."""
+    """Time ``flash_attention`` against standard attention (fp32 scores, softmax, fp16
+    P @ V -- the reference's comparison formula) on seeded fp16 N(0,1) inputs.
+
+    Returns the reference's keys (config, flash_ms, std_ms, speedup, flash_mem_mb,
+    std_mem_mb, mem_savings_pct; memory is what one call needs beyond its inputs)
+    plus flash_tflops and flash_frac_peak (FA2 flop convention, 4*B*H*N^2*d, halved
+    when causal, against the device's dense fp16 MFMA peak), std_tflops and
+    max_abs_diff between the two outputs."""
     from .flash_attn import flash_attention
 
-    device = torch.device("cuda")
-    q = torch.randn(batch_size, num_heads, seq_len, head_dim, device=device, dtype=torch.float16)
-    k = torch.randn_like(q)
-    v = torch.randn_like(q)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    gen = torch.Generator().manual_seed(0)
+    shape = (batch_size, num_heads, seq_len, head_dim)
+    q, k, v = (torch.randn(shape, generator=gen).half().to(dev) for _ in range(3))
+    scale = 1.0 / math.sqrt(head_dim)
+    future = (torch.triu(torch.ones(seq_len, seq_len, dtype=torch.bool, device=dev), diagonal=1)
+              if is_causal else None)
 
-    def std_attn(q, k, v):
-        scale = 1.0 / (head_dim ** 0.5)
-        s = torch.matmul(q.float(), k.float().transpose(-2, -1)) * scale
-        if is_causal:
-            mask = torch.triu(torch.ones(seq_len, seq_len, device=device, dtype=torch.bool), diagonal=1)
-            s.masked_fill_(mask, float("-inf"))
-        return torch.matmul(torch.softmax(s, dim=-1).half(), v)
+    def flash():
+        return flash_attention(q, k, v, softmax_scale=scale, is_causal=is_causal)
 
-    for _ in range(num_warmup):
-        flash_attention(q, k, v, is_causal=is_causal)
-        std_attn(q, k, v)
-    torch.cuda.synchronize()
+    def standard():
+        s = (q.float() @ k.float().transpose(-1, -2)) * scale
+        if future is not None:
+            s = s.masked_fill(future, float("-inf"))
+        return torch.softmax(s, dim=-1).half() @ v
 
-    torch.cuda.reset_peak_memory_stats()
-    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s_ev.record()
-    for _ in range(num_iters):
-        flash_attention(q, k, v, is_causal=is_causal)
-    e_ev.record()
-    torch.cuda.synchronize()
-    flash_ms = s_ev.elapsed_time(e_ev) / num_iters
-    flash_mem = torch.cuda.max_memory_allocated() / 1e6
+    diff = float((flash().float() - standard().float()).abs().max())
+    flash_ms = _event_ms(flash, num_warmup, num_iters)
+    std_ms = _event_ms(standard, num_warmup, num_iters)
+    flash_mb, std_mb = _peak_mb(flash), _peak_mb(standard)
 
-    torch.cuda.reset_peak_memory_stats()
-    s_ev.record()
-    for _ in range(num_iters):
-        std_attn(q, k, v)
-    e_ev.record()
-    torch.cuda.synchronize()
-    std_ms = s_ev.elapsed_time(e_ev) / num_iters
-    std_mem = torch.cuda.max_memory_allocated() / 1e6
-
+    flops = 4.0 * batch_size * num_heads * seq_len * seq_len * head_dim * (0.5 if is_causal else 1.0)
+    peak = get_device_info(dev.index)["peak_fp16_tflops"]
+    flash_tflops = flops / (flash_ms * 1e-3) / 1e12
     return {
-        "config": f"B={batch_size} H={num_heads} N={seq_len} d={head_dim}",
-        "flash_ms": round(flash_ms, 3), "std_ms": round(std_ms, 3),
-        "speedup": round(std_ms / flash_ms, 2) if flash_ms > 0 else 0,
-        "flash_mem_mb": round(flash_mem, 1), "std_mem_mb": round(std_mem, 1),
-        "mem_savings_pct": round((1 - flash_mem / std_mem) * 100, 1) if std_mem > 0 else 0,
+        "config": f"B={batch_size} H={num_heads} N={seq_len} d={head_dim}" + (" causal" if is_causal else ""),
+        "flash_ms": round(flash_ms, 3),
+        "std_ms": round(std_ms, 3),
+        "speedup": round(std_ms / flash_ms, 2) if flash_ms > 0 else 0.0,
+        "flash_tflops": round(flash_tflops, 1),
+        "flash_frac_peak": round(flash_tflops / peak, 4) if peak else None,
+        "std_tflops": round(flops / (std_ms * 1e-3) / 1e12, 1),
+        "flash_mem_mb": round(flash_mb, 1),
+        "std_mem_mb": round(std_mb, 1),
+        "mem_savings_pct": round(100.0 * (1.0 - flash_mb / std_mb), 1) if std_mb > 0 else 0.0,
+        "max_abs_diff": round(diff, 5),
     }
