@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "fal_kernels.h"
@@ -583,6 +584,68 @@ int fal_decode_bf16(const void* q, const void* k_cache, const void* v_cache, con
   return fal_decode_impl(q, k_cache, v_cache, cache_seqlens, mask_bias, mask_stride, o, lse, batch, heads_q,
                          heads_kv, head_dim, max_seqlen_k, q_strides, k_strides, v_strides, o_strides,
                          softmax_scale, workspace, workspace_bytes, stream, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Decode without allocation: the workspace is a fixed device array of this file
+// ---------------------------------------------------------------------------
+}  // extern "C"
+
+namespace {
+
+// Workspace of fal_decode_noalloc: partial outputs, partial LSEs and the work list of
+// one decode call.  Each GPU that runs the entry point holds its own copy until the
+// process ends; every call on that GPU shares it.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];   // device address of `scratch` on each device, once resolved
+
+// The device address of this device's `scratch` (the host-side symbol is only a handle).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FAL_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FAL_ERR_UNSUPPORTED, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(FAL_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FAL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fal_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, const int32_t* cache_seqlens,
+                       const float* mask_bias, int64_t mask_stride, void* o, float* lse, int64_t batch,
+                       int64_t heads_q, int64_t heads_kv, int64_t head_dim, int64_t max_seqlen_k,
+                       const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                       const int64_t* o_strides, float softmax_scale, void* stream) {
+  if (!head_dim_ok(head_dim))
+    return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
+  if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(max_seqlen_k))
+    return fail(FAL_ERR_INVALID, "invalid sizes");
+  const size_t need = fal_decode_workspace_size(batch, heads_q, heads_kv, max_seqlen_k, head_dim);
+  if (need > kNoAllocScratchBytes)
+    return fail(FAL_ERR_WORKSPACE,
+                "fal_decode_noalloc: this call needs %zu bytes of workspace, above the fixed %zu-byte "
+                "device array (use fal_decode with a caller workspace)",
+                need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return fal_decode_impl(q, k_cache, v_cache, cache_seqlens, mask_bias, mask_stride, o, lse, batch, heads_q,
+                         heads_kv, head_dim, max_seqlen_k, q_strides, k_strides, v_strides, o_strides,
+                         softmax_scale, ws, kNoAllocScratchBytes, stream, 0);
 }
 
 }  // extern "C"

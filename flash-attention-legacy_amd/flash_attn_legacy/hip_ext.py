@@ -62,6 +62,7 @@ def _load() -> ctypes.CDLL:
         "fal_bwd_varlen": (_INT, [_VP] * 11 + [_I64] * 8 + [_STR] * 8 + [_F32, _INT, _VP, _SZ, _VP]),
         "fal_decode_workspace_size": (_SZ, [_I64] * 5),
         "fal_decode": (_INT, [_VP] * 5 + [_I64, _VP, _VP] + [_I64] * 5 + [_STR] * 4 + [_F32, _VP, _SZ, _VP]),
+        "fal_decode_noalloc": (_INT, [_VP] * 5 + [_I64, _VP, _VP] + [_I64] * 5 + [_STR] * 4 + [_F32, _VP]),
     }
     for name in ("fal_fwd", "fal_fwd_varlen", "fal_bwd", "fal_bwd_varlen", "fal_decode"):
         sig[name + "_bf16"] = sig[name]   # bf16 forms: same arguments
@@ -81,6 +82,7 @@ SYMBOLS = (
     "fal_bwd_workspace_size", "fal_bwd", "fal_bwd_varlen_workspace_size", "fal_bwd_varlen",
     "fal_decode_workspace_size", "fal_decode",
     "fal_fwd_bf16", "fal_fwd_varlen_bf16", "fal_bwd_bf16", "fal_bwd_varlen_bf16", "fal_decode_bf16",
+    "fal_decode_noalloc",
 )
 
 

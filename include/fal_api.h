@@ -210,6 +210,30 @@ int fal_decode_bf16(const void* q, const void* k_cache, const void* v_cache,
                     const int64_t* v_strides, const int64_t* o_strides,
                     float softmax_scale, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * fal_decode without a workspace argument and without any allocation.
+ * No counterpart in the reference.  It serves callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Arguments, results and status codes are those of fal_decode (fp16),
+ * minus workspace / workspace_bytes.
+ *   - The workspace is a fixed 16 MiB device array inside the library (one copy per
+ *     GPU, held until the process ends).  A call whose fal_decode_workspace_size
+ *     exceeds 16 MiB fails with FAL_ERR_WORKSPACE (e.g. batch 32, 32 query heads,
+ *     d 128 allows caches up to 32768 rows per sequence at the default split size).
+ *   - Every call on one GPU shares that array: calls that overlap in time on one GPU
+ *     (different streams or threads) race and give wrong results.  Serialise them.
+ *   - The first call on each device looks up the array's device address; no
+ *     allocation, free or memset happens in any call.
+ */
+int fal_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* cache_seqlens, const float* mask_bias, int64_t mask_stride,
+                       void* o, float* lse,
+                       int64_t batch, int64_t heads_q, int64_t heads_kv, int64_t head_dim,
+                       int64_t max_seqlen_k,
+                       const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides,
+                       float softmax_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
