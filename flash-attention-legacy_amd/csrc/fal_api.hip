@@ -96,10 +96,18 @@ int fal_device_supported(int device) {
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
+size_t fal_fwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
+                              int is_causal) {
+  if (!head_dim_ok(head_dim) || batch <= 0 || heads_q <= 0 || !dims_ok(seqlen_q) || !dims_ok(seqlen_k)) return 0;
+  int kchunk, nsplit;
+  return fwd_split_plan(batch, heads_q, seqlen_q, seqlen_k, (int)head_dim, is_causal != 0, &kchunk, &nsplit);
+}
+
 static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
             int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream, int bf16) {
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* workspace, size_t workspace_bytes,
+            void* stream, int bf16) {
   if (!head_dim_ok(head_dim))
     return fail(FAL_ERR_UNSUPPORTED, "head_dim must be 32, 64, 96, 128, or 256, got %lld", (long long)head_dim);
   if (batch < 0 || heads_q <= 0 || heads_kv <= 0 || !dims_ok(seqlen_q) || !dims_ok(seqlen_k))
@@ -131,25 +139,39 @@ static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, fl
   p.scale_log2 = signed_scale_log2(softmax_scale);
   const int bm = fwd_block_m((int)head_dim);
   p.n_qtiles = cdiv((int)seqlen_q, bm);
-  const int64_t nblocks = (int64_t)p.n_qtiles * batch * heads_q;
+  // small grids split the key range (partials in the workspace, merged by a second kernel)
+  const size_t need = fwd_split_plan(batch, heads_q, seqlen_q, seqlen_k, (int)head_dim, is_causal != 0, &p.kchunk,
+                                     &p.nsplit);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
+  if (p.kchunk) {
+    p.part_o = static_cast<float*>(workspace);
+    p.part_ml = p.part_o + (size_t)batch * heads_q * p.nsplit * seqlen_q * head_dim;
+  }
+  const int64_t nblocks = (int64_t)p.n_qtiles * batch * heads_q * p.nsplit;
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
-  return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks),
-                                  static_cast<hipStream_t>(stream)),
-                       "fal_fwd");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), st);
+  if (e == hipSuccess && p.kchunk) e = launch_fwd_combine(p, (int)head_dim, is_causal != 0, st);
+  return launch_status(e, "fal_fwd");
 }
 int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
             int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream) {
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* workspace,
+            size_t workspace_bytes, void* stream) {
   return fal_fwd_impl(q, k, v, o, lse, batch, heads_q, heads_kv, seqlen_q, seqlen_k, head_dim, q_strides,
-                      k_strides, v_strides, o_strides, softmax_scale, is_causal, stream, 0);
+                      k_strides, v_strides, o_strides, softmax_scale, is_causal, workspace, workspace_bytes,
+                      stream, 0);
 }
 int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
             int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-            const int64_t* o_strides, float softmax_scale, int is_causal, void* stream) {
+            const int64_t* o_strides, float softmax_scale, int is_causal, void* workspace,
+            size_t workspace_bytes, void* stream) {
   return fal_fwd_impl(q, k, v, o, lse, batch, heads_q, heads_kv, seqlen_q, seqlen_k, head_dim, q_strides,
-                      k_strides, v_strides, o_strides, softmax_scale, is_causal, stream, 1);
+                      k_strides, v_strides, o_strides, softmax_scale, is_causal, workspace, workspace_bytes,
+                      stream, 1);
 }
 
 size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q, int64_t head_dim) {
@@ -349,7 +371,7 @@ static int fal_bwd_impl(const void* dout, const void* q, const void* k, const vo
   p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;
   p.Nq = (int)seqlen_q; p.Nk = (int)seqlen_k;
   p.scale = softmax_scale;
-  p.scale_log2 = softmax_scale * kLog2e;
+  p.scale_log2 = signed_scale_log2(softmax_scale);
   const int bn = bwd_block_n((int)head_dim);
   p.n_ktiles = cdiv((int)seqlen_k, bn);
   const int64_t nblocks = (int64_t)p.n_ktiles * batch * heads_kv;
@@ -435,7 +457,7 @@ static int fal_bwd_varlen_impl(const void* dout, const void* q, const void* k, c
   p.total_q = (int)total_q;
   p.total_k = (int)total_k;
   p.scale = softmax_scale;
-  p.scale_log2 = softmax_scale * kLog2e;
+  p.scale_log2 = signed_scale_log2(softmax_scale);
   p.cu_q = cu_seqlens_q;
   p.cu_k = cu_seqlens_k;
   p.work = work;

@@ -391,8 +391,9 @@ bwd_kernel(BwdParams p) {
 // S = Q K^T and dP = dO V^T for its 32 keys x 32 rows, P = exp2(S - L*log2e),
 // dS = P (dP - D), then dV^T += dO^T P and dK^T += Q^T dS in registers (Q^T, dO^T
 // read transposed from LDS, P and dS taken from the accumulators as B operands).
-//   - The dP accumulator starts at -D, so the MFMAs produce dP - D directly; the
-//     exponent of P is one FMA, S*scale*log2e - L*log2e.
+//   - The S accumulator starts at -L*log2e / c (c = scale*log2e) and the dP
+//     accumulator at -D, so the MFMAs produce the exponent of P over c and dP - D
+//     directly: one multiply and an exp2 per element.
 //   - Operands of MFMA step t+1 are read before the MFMAs of step t.
 //   - Only tiles that straddle the diagonal apply the causal mask.
 //   - MFMA phases run at raised wave priority, so a SIMD's other wave fills their
@@ -405,13 +406,13 @@ bwd_kernel(BwdParams p) {
 #ifndef FAL_BWD2_NW
 #define FAL_BWD2_NW 4   // waves per workgroup: 4 (64 keys, 2 workgroups per CU) or 8 (128 keys, double-buffered Q/dO)
 #endif
-template <class T, int D, bool CAUSAL>
+template <class T, int D, bool CAUSAL, bool FUSED>
 __global__ void __launch_bounds__(FAL_BWD2_NW * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
 bwd2_kernel(BwdParams p) {
   using V8 = vec8<T>;
   using V4 = vec4<T>;
-  // K stays exact and scale*log2(e) and -L*log2e are applied to the fp32 scores with
-  // one FMA each.  FAL_PRESCALE_FP16 instead pre-multiplies an fp16 K tile in LDS
+  // K stays exact and scale*log2(e) is applied to the fp32 scores (one multiply).
+  // FAL_PRESCALE_FP16 instead pre-multiplies an fp16 K tile in LDS
   // (rounded once) and starts the S accumulator at -L*log2e; that rounding costs
   // accuracy at large logits, so it is off.
   constexpr bool PRESCALE = FAL_PRESCALE_FP16 && std::is_same<T, half_t>::value;
@@ -428,12 +429,17 @@ bwd2_kernel(BwdParams p) {
   constexpr int QIPT = BMQ * CPR / (NW * 64);
   static_assert(BMQ * CPR % (NW * 64) == 0, "Q tile must split evenly over the waves");
   static_assert((DBUF ? 2 : 1) * 2 * QPART * 2 >= NKG * 32 * D * 4, "dK/dV reduction reuses the Q/dO buffers");
+  static_assert(!(FUSED && PRESCALE), "the fused dQ product needs the unscaled K tile");
+  static_assert(!FUSED || NW == 4, "the fused dQ product splits 64 rows x D over four waves");
+  constexpr int LDQ = BMQ + 8;            // dS^T tile row stride (fused): 64 query rows + pad
 
   __shared__ __attribute__((aligned(1024))) T ks_s[KPART];
   __shared__ __attribute__((aligned(1024))) T vs_s[KPART];
   __shared__ __attribute__((aligned(1024))) T qd_s[(DBUF ? 2 : 1) * 2 * QPART];   // [buffer][Q, dO]
   __shared__ float l_s[2][BMQ];
   __shared__ float d_s[2][BMQ];
+  // fused: dS^T of the current item, row = key of the tile, column = query row of the item
+  __shared__ __attribute__((aligned(16))) T dst_s[FUSED ? BN * LDQ : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -601,6 +607,9 @@ bwd2_kernel(BwdParams p) {
           nl = (L == -INFINITY) ? -INFINITY : -L * kLog2e;
           nd = -p.delta[o];
         }
+        // without the K pre-scale the S accumulator starts at -L*log2e / c, so that
+        // c * S is the exponent (a row with L = -inf keeps exponent -inf for either sign of c)
+        if (!PRESCALE) nl /= c;
         lpre = nl;
         dpre = nd;
       }
@@ -608,11 +617,17 @@ bwd2_kernel(BwdParams p) {
 
     if (nitems_q > 0) fetch(0);
     int c_qt = qt0;   // query tile of the current item
+    int c_hq = 0;     // its query head within the group
     for (int item = 0; item < nitems_q; ++item) {
       {
         const int buf = DBUF ? (item & 1) : 0;
         const int q0 = c_qt * BMQ;
-        if (++c_qt == nqt) c_qt = qt0;
+        const int cur_hq = c_hq;
+        if (++c_qt == nqt) {
+          c_qt = qt0;
+          ++c_hq;
+        }
+        (void)cur_hq;
         wait_vmcnt0();
         if (tid < BMQ) {
           l_s[buf][tid] = lpre;
@@ -624,7 +639,7 @@ bwd2_kernel(BwdParams p) {
         const T* do_s = qd_s + (buf * 2 + 1) * QPART + qh * 32 * CPR * 8;
         const int qr0 = q0 + qh * 32;     // first query row of this wave's half
         if (!CAUSAL || qr0 + 31 >= kw0) {
-          // S = Q K^T - L*log2e and dP = dO V^T - D
+          // S = Q K^T - L*log2e/c and dP = dO V^T - D
           f32x16 s, dp;
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
@@ -632,7 +647,7 @@ bwd2_kernel(BwdParams p) {
             const f32x4 dn = *reinterpret_cast<const f32x4*>(&d_s[buf][qh * 32 + g4 * 8 + hh * 4]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              s[g4 * 4 + e] = PRESCALE ? ln[e] : 0.f;
+              s[g4 * 4 + e] = ln[e];
               dp[g4 * 4 + e] = dn[e];
             }
           }
@@ -669,13 +684,7 @@ bwd2_kernel(BwdParams p) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int i = g4 * 4 + e;
-                float pv;
-                if (PRESCALE) {
-                  pv = fast_exp2(s[i]);
-                } else {
-                  const float ln = l_s[buf][qh * 32 + g4 * 8 + hh * 4 + e];
-                  pv = fast_exp2(fmaf(s[i], c, ln));
-                }
+                float pv = fast_exp2(PRESCALE ? s[i] : s[i] * c);
                 if (decltype(masked)::value && cthr > g4 * 8 + e) pv = 0.f;
                 s[i] = pv;
                 dp[i] = pv * dp[i];
@@ -710,6 +719,52 @@ bwd2_kernel(BwdParams p) {
             }
           }
           __builtin_amdgcn_s_setprio(0);
+          if constexpr (FUSED) {
+            // this wave's dS^T block (32 keys x 32 query rows) into the tile
+            T* drow = dst_s + (kg * 32 + l32) * LDQ + qh * 32 + hh * 4;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              V4 h;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) h[e] = (T)dp[g4 * 4 + e];
+              *reinterpret_cast<V4*>(drow + g4 * 8) = h;
+            }
+          }
+        } else if constexpr (FUSED) {
+          // every key of this wave is past every query row of its half: dS = 0
+          T* drow = dst_s + (kg * 32 + l32) * LDQ + qh * 32 + hh * 4;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) *reinterpret_cast<u32x2*>(drow + g4 * 8) = u32x2{0, 0};
+        }
+        if constexpr (FUSED) {
+          // dQ[q, :] += dS[q, keys] K[keys, :] over the tile's 64 keys, added to the fp32
+          // accumulator with atomics (the reference's scheme, flash_attn_bwd.cu:602-620).
+          // Wave (kg, qh) takes query half qh and head-dim columns kg*D/2 .. +D/2.
+          __syncthreads();                // barrier C: the dS^T tile is complete
+          constexpr int QDB = D / 64;     // 32-wide head-dim blocks per wave
+          const int tofs_s = tr_offset(lane, LDQ) + qh * 32;
+          // one buffer resource over the item's accumulator rows: adds to rows past the
+          // end of the sequence fall outside it and are dropped
+          const float* qa = p.dq_acc + (int64_t)b * p.dqa_sb + (int64_t)(hkv * G + cur_hq) * p.dqa_sh +
+                            (int64_t)(q_off + q0) * p.dqa_ss;
+          const __amdgpu_buffer_rsrc_t qrs =
+              make_rsrc(qa, (uint32_t)min((int64_t)max(nq - q0, 0) * p.dqa_ss * 4, (int64_t)0x7fffffff));
+          // lane part of the byte offset in a VGPR, the row step of element i in the
+          // instruction's scalar offset
+          const int qrow_bytes = __builtin_amdgcn_readfirstlane((int)p.dqa_ss * 4);
+          const int qoff = ((qh * 32 + hh * 4) * (int)p.dqa_ss + kg * QDB * 32 + l32) * 4;
+#pragma unroll
+          for (int j = 0; j < QDB; ++j) {
+            // one 32-column block at a time (16 accumulator registers)
+            f32x16 qacc = zero_f16();
+#pragma unroll
+            for (int ks = 0; ks < BN / 16; ++ks)
+              qacc = mfma32(kslab_tr(dst_s + tofs_s, ks * 16, hh, LDQ), trk(ks_s, kg * QDB + j, ks * 16), qacc);
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(qacc[i], qrs, qoff + j * 128,
+                                                              ((i >> 2) * 8 + (i & 3)) * qrow_bytes, 0);
+          }
         }
         if (!DBUF && item + 1 < nitems_q) {
           __syncthreads();                // barrier B: every wave is done with this item's tile
@@ -1030,6 +1085,12 @@ constexpr int kBwdNW = 4;
 // head dims on the split path (dQ kernel + dK/dV kernel); 256 keeps the atomic kernel,
 // whose dK/dV accumulators would not fit the split kernel's registers
 constexpr bool split_d(int d) { return d == 32 || d == 64 || d == 96 || d == 128; }
+// head dims whose KV-outer kernel also forms dQ = dS K (fp32 atomics into an accumulator,
+// five products instead of the split form's seven)
+#ifndef FAL_BWD_FUSED
+#define FAL_BWD_FUSED 0
+#endif
+constexpr bool fused_d(int d) { return FAL_BWD_FUSED && (d == 64 || d == 128); }
 
 int bwd_block_n(int d) {
   return split_d(d) ? FAL_BWD2_NW * 16 : kBwdNW * 32;
@@ -1038,12 +1099,13 @@ int bwd_block_n(int d) {
 template <class T, int D>
 static hipError_t launch_bwd_t(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
   if constexpr (split_d(D)) {
+    constexpr bool kFused = fused_d(D);
     // batched causal: one workgroup per pair of key tiles
     if (!p.cu_q && causal) grid.x = (unsigned)((p.n_ktiles + 1) / 2) * p.B * p.Hkv;
     if (causal)
-      hipLaunchKernelGGL((bwd2_kernel<T, D, true>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
+      hipLaunchKernelGGL((bwd2_kernel<T, D, true, kFused>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
     else
-      hipLaunchKernelGGL((bwd2_kernel<T, D, false>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
+      hipLaunchKernelGGL((bwd2_kernel<T, D, false, kFused>), grid, dim3(FAL_BWD2_NW * 64), 0, st, p);
   } else {
     if (causal)
       hipLaunchKernelGGL((bwd_kernel<T, D, kBwdNW, 32, true>), grid, dim3(kBwdNW * 64), 0, st, p);
@@ -1062,7 +1124,7 @@ static hipError_t launch_bwd_d(const BwdParams& p, int causal, dim3 grid, hipStr
 #endif
 constexpr int kDqNW = 4;
 
-bool bwd_split_dq(int d) { return split_d(d); }
+bool bwd_split_dq(int d) { return split_d(d) && !fused_d(d); }
 int bwd_dq_block_m(int d) {
   (void)d;
   return kDqNW * 32;

@@ -5,8 +5,10 @@
 // s = q k^T * scale (+ additive mask), softmax over the keys, @ v.  This file computes
 // the same result without materialising the repeated K/V or the score row.
 //
-// Schedule kernel: turns cache_seqlens into a longest-first list of (sequence, split)
-// work items on the device (no host synchronisation).
+// Work items (sequence, split): for batches of up to 64 sequences each split workgroup
+// derives its own item from cache_seqlens (full splits first); larger batches use a
+// schedule kernel that builds a longest-first list on the device.  Neither needs a
+// host synchronisation.
 // Split kernel: one workgroup per (work item, KV head, group of up to 16 query heads)
 // covers `chunk` cache rows.
 // * The query heads of the KV head ride in one 16x16x32 MFMA tile: S^T = K Q^T with
@@ -59,6 +61,42 @@ __device__ __forceinline__ int vswz(int r) {
   return D == 96 ? (r & 3) : (r & ((D / 8 < 16 ? D / 8 : 16) - 1));
 }
 
+// Work item `item` for a batch of at most 64 sequences, computed by every wave from
+// cache_seqlens (one load per lane), so no schedule kernel runs first: every full split
+// of every sequence (sequence-major), then the shorter last splits, longest first (ties
+// in sequence order), as the schedule kernel orders them.  False past the last item.
+__device__ __forceinline__ bool decode_item_small(const DecodeParams& p, int item, int& b, int& split) {
+  const int lane = threadIdx.x & 63;
+  const int L = lane < p.B ? min(max(p.seqlens[lane], 0), p.max_seqlen) : 0;
+  const int nf = L / p.chunk;
+  int inc = nf;   // inclusive prefix sum of the full splits over the sequences
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  const int F = __shfl(inc, 63);
+  if (item < F) {
+    const int bl = __builtin_ctzll(__ballot(inc > item));
+    b = bl;
+    split = item - (__shfl(inc, bl) - __shfl(nf, bl));
+    return true;
+  }
+  const int rem = L % p.chunk;
+  const unsigned long long part = __ballot(rem != 0);
+  const int j = item - F;
+  if (j >= __popcll(part)) return false;
+  int rank = 0;
+  for (int k = 0; k < p.B; ++k) {
+    const int rk = __builtin_amdgcn_readlane(rem, k);
+    rank += (rk > rem || (rk == rem && k < lane)) ? 1 : 0;
+  }
+  const int bl = __builtin_ctzll(__ballot(rem != 0 && rank == j));
+  b = bl;
+  split = __shfl(nf, bl);
+  return true;
+}
+
 template <class T, int D, int NW>
 __global__ void __launch_bounds__(NW * 64)
 decode_split_kernel(DecodeParams p) {
@@ -77,10 +115,17 @@ decode_split_kernel(DecodeParams p) {
 
   const int nhg = cdiv(p.Hq / p.Hkv, 16);
   const int heads_tiles = p.Hkv * nhg;
-  const int2 wk = p.work[blockIdx.x / heads_tiles];
-  if (wk.x < 0) return;
-  const int b = wk.x;
-  const int split = wk.y;
+  int b, split;
+  if (p.work) {
+    const int2 wk = p.work[blockIdx.x / heads_tiles];
+    if (wk.x < 0) return;
+    b = wk.x;
+    split = wk.y;
+  } else {
+    if (!decode_item_small(p, (int)(blockIdx.x / heads_tiles), b, split)) return;
+    b = __builtin_amdgcn_readfirstlane(b);
+    split = __builtin_amdgcn_readfirstlane(split);
+  }
   const int hkv = (blockIdx.x % heads_tiles) / nhg;
   const int hg = (blockIdx.x % heads_tiles) % nhg;
   const int L = min(max(p.seqlens[b], 0), p.max_seqlen);
@@ -375,14 +420,24 @@ int decode_chunk(int d, int B, int Hkv, int max_seqlen) {
   return chunk < tile ? tile : chunk;
 }
 
+#ifndef FAL_DEC_INLINE_ITEMS
+#define FAL_DEC_INLINE_ITEMS 1   // batches of <= 64 sequences: work items computed in the split kernel
+#endif
+
+
 template <class T, int D>
-static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t st) {
+static hipError_t launch_decode_t(const DecodeParams& pin, hipStream_t st) {
+  DecodeParams p = pin;
   const int nhg = cdiv(p.Hq / p.Hkv, 16);
   const int capacity = p.B * p.max_splits;
-  hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(1024), 0, st, p.seqlens, p.B, p.max_seqlen, p.chunk,
-                     const_cast<int2*>(p.work), capacity);
-  hipError_t e0 = hipGetLastError();
-  if (e0 != hipSuccess) return e0;
+  if (FAL_DEC_INLINE_ITEMS && p.B <= 64) {
+    p.work = nullptr;
+  } else {
+    hipLaunchKernelGGL(decode_schedule_kernel, dim3(1), dim3(1024), 0, st, p.seqlens, p.B, p.max_seqlen, p.chunk,
+                       const_cast<int2*>(p.work), capacity);
+    hipError_t e0 = hipGetLastError();
+    if (e0 != hipSuccess) return e0;
+  }
   hipLaunchKernelGGL((decode_split_kernel<T, D, FAL_DEC_NW>), dim3((unsigned)capacity * p.Hkv * nhg),
                      dim3(FAL_DEC_NW * 64), 0, st, p);
   hipError_t e = hipGetLastError();

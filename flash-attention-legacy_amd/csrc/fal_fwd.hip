@@ -21,6 +21,7 @@
 //   V^T comes from the row-major V tile through ds_read_b64_tr_b16;
 // * causal tiles above the diagonal are never visited; fully-masked waves inside a
 //   diagonal tile skip their MFMAs.
+#include <algorithm>
 #include <type_traits>
 
 #include "fal_kernels.h"
@@ -44,7 +45,7 @@ namespace fal {
 
 // A workgroup's (batch or sequence, query head, query tile) and its row ranges.
 struct FwdItem {
-  int b, hq, qt, q_off, k_off, nq, nk;
+  int b, hq, qt, q_off, k_off, nq, nk, split;
 };
 
 // Resolves the work item of this workgroup; false for a padding block, which exits.
@@ -65,6 +66,7 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
     if (wk.x < 0) return false;
     it.hq = (grp % p.Hkv) * g + k8 % g;
     it.b = 0;
+    it.split = 0;
     it.qt = wk.y;
     seg_bounds(p.cu_q, wk.x, p.total_q, it.q_off, it.nq);
     seg_bounds(p.cu_k, wk.x, p.total_k, it.k_off, it.nk);
@@ -75,6 +77,8 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
     const int total = gridDim.x;
     int id = blockIdx.x;
     if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+    it.split = id % p.nsplit;   // the splits of a query tile run next to each other
+    id /= p.nsplit;
     const int g = p.Hq / p.Hkv;
     const int hg = id % g;
     int rest = id / g;
@@ -154,9 +158,14 @@ fwd_kernel(FwdParams p) {
     }
   }
 
-  // ---- key range ----
+  // ---- key range: tiles [jbeg, jend), the whole range or this workgroup's split ----
   const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
-  const int ntiles = cdiv(kend, BN);
+  int jbeg = 0, jend = cdiv(kend, BN);
+  if (p.kchunk) {
+    jbeg = it.split * p.kchunk;
+    jend = min(jend, jbeg + p.kchunk);
+    if (jbeg >= jend && it.split > 0) return;   // split past this tile's keys (split 0 always reports)
+  }
   // tiles below this index need no masking for any row of the workgroup
   const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
 
@@ -216,15 +225,17 @@ fwd_kernel(FwdParams p) {
     for (int i = 0; i < DB; ++i) oacc[rb][i] = zero_f16();
   // m_run: reference max of the row (log2 domain); it may lag the true running max, as
   // long as every p = exp2(s - m_run) of a tile fits fp16 (the tile's p sum <= 2^15).
-  // negm: -m_run broadcast over an accumulator block (the addend of the score FMA, or
-  // the starting value of S^T under FAL_PRESCALE_FP16).
+  // nm: -m_run, the addend of the score FMA; negm: the same broadcast over an
+  // accumulator block, the starting value of S^T under FAL_PRESCALE_FP16.
   float m_run[RB], l_run[RB];
   f32x16 negm[RB];
+  float nm[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     m_run[rb] = -INFINITY;
     l_run[rb] = 0.f;
     negm[rb] = zero_f16();
+    nm[rb] = 0.f;
   }
 
   auto tile_body = [&](auto masked, int j, int buf) {
@@ -262,7 +273,7 @@ fwd_kernel(FwdParams p) {
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) sacc[rb][kb][i] = fmaf(sacc[rb][kb][i], c, negm[rb][i]);
+          for (int i = 0; i < 16; ++i) sacc[rb][kb][i] = fmaf(sacc[rb][kb][i], c, nm[rb]);
     }
     if (MASK) {
 #pragma unroll
@@ -328,9 +339,11 @@ fwd_kernel(FwdParams p) {
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) sacc[rb][kb][i] -= dlt;
-        const float nm = (m_run[rb] == -INFINITY) ? 0.f : -m_run[rb];
+        nm[rb] = (m_run[rb] == -INFINITY) ? 0.f : -m_run[rb];
+        if (PRESCALE) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) negm[rb][i] = nm;
+          for (int i = 0; i < 16; ++i) negm[rb][i] = nm[rb];
+        }
       }
       make_p();
     }
@@ -353,30 +366,54 @@ fwd_kernel(FwdParams p) {
   auto step = [&](auto masked, int j, int buf) {
     wait_vmcnt0();
     __syncthreads();                       // tile j visible; tile j-1 reads finished
-    if (j + 1 < ntiles) load_tile(j + 1, buf ^ 1);
+    if (j + 1 < jend) load_tile(j + 1, buf ^ 1);
     tile_body(masked, j, buf);
   };
 
-  if (ntiles > 0) load_tile(0, 0);
+  if (jbeg < jend) load_tile(jbeg, 0);
   // Tiles that need no mask for any row of the workgroup: straight-line, unrolled by
-  // two so both LDS buffer offsets are constants.
-  int j = 0;
-  for (; j + 1 < nfull; j += 2) {
+  // two so both LDS buffer offsets are constants (tile j uses buffer (j - jbeg) & 1).
+  const int fend = min(nfull, jend);
+  int j = jbeg;
+  for (; j + 1 < fend; j += 2) {
     step(std::false_type{}, j, 0);
     step(std::false_type{}, j + 1, 1);
   }
-  if (j < nfull) {
+  if (j < fend) {
     step(std::false_type{}, j, 0);
     ++j;
   }
   // Diagonal and tail tiles; waves whose rows all precede the tile only keep the
   // pipeline (barrier + prefetch) going.
   const int wrow_hi = m0 + (w * RB + RB - 1) * 32 + 31;   // last query row of this wave
-  for (; j < ntiles; ++j) {
+  for (; j < jend; ++j) {
     wait_vmcnt0();
     __syncthreads();
-    if (j + 1 < ntiles) load_tile(j + 1, (j + 1) & 1);
-    if (!CAUSAL || j * BN <= wrow_hi) tile_body(std::true_type{}, j, j & 1);
+    if (j + 1 < jend) load_tile(j + 1, (j + 1 - jbeg) & 1);
+    if (!CAUSAL || j * BN <= wrow_hi) tile_body(std::true_type{}, j, (j - jbeg) & 1);
+  }
+
+  if (p.kchunk) {
+    // split-KV: this split's unnormalised O, its reference max m and its sum l
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float l_tot = pair_sum(l_run[rb]);
+      if (row[rb] < nq) {
+        const int64_t prow = ((int64_t)(b * p.Hq + hq) * p.nsplit + it.split) * p.Nq + row[rb];
+        float* po = p.part_o + prow * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            f32x4 x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = oacc[rb][db][g4 * 4 + e];
+            *reinterpret_cast<f32x4*>(po + db * 32 + g4 * 8 + hh * 4) = x;
+          }
+        if (hh == 0) *reinterpret_cast<float2*>(p.part_ml + prow * 2) = make_float2(m_run[rb], l_tot);
+      }
+    }
+    return;
   }
 
   // ---- epilogue: normalise, write O and L ----
@@ -402,6 +439,57 @@ fwd_kernel(FwdParams p) {
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV combine: one group of D/8 lanes per query row merges the row's splits,
+// O = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s with M = max_s m_s, and writes
+// O and L = (M + log2 sum) * ln 2 (-inf for a row with no visible key).
+// ---------------------------------------------------------------------------
+template <class T, int D, int BM, int BN, bool CAUSAL>
+__global__ void __launch_bounds__(256)
+fwd_combine_kernel(FwdParams p) {
+  constexpr int G = D / 8;              // lanes per row, 8 columns each
+  if (threadIdx.x >= (256 / G) * G) return;
+  const int r = blockIdx.x * (256 / G) + threadIdx.x / G;
+  const int c = (threadIdx.x % G) * 8;
+  const int rows = p.B * p.Hq * p.Nq;
+  if (r >= rows) return;
+  const int n = r % p.Nq;
+  const int bh = r / p.Nq;
+  const int m0 = (n / BM) * BM;
+  const int kend = CAUSAL ? min(p.Nk, m0 + BM) : p.Nk;
+  const int ns = max(1, cdiv(cdiv(kend, BN), p.kchunk));
+  const int64_t base = (int64_t)bh * p.nsplit * p.Nq + n;   // split s: base + s * Nq
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, p.part_ml[(base + (int64_t)s * p.Nq) * 2]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float lsum = 0.f;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const int64_t pr = base + (int64_t)s * p.Nq;
+    const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + pr * 2);
+    const float wgt = ml.y > 0.f ? fast_exp2(ml.x - Mu) : 0.f;
+    lsum = fmaf(wgt, ml.y, lsum);
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(p.part_o + pr * D + c);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(p.part_o + pr * D + c + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] = fmaf(wgt, x0[e], acc[e]);
+      acc[e + 4] = fmaf(wgt, x1[e], acc[e + 4]);
+    }
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const int b = bh / p.Hq, hq = bh % p.Hq;
+  vec8<T> h;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = (T)(acc[e] * inv);
+  st_u4((T*)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)n * p.o_ss + c, __builtin_bit_cast(u32x4, h));
+  if (c == 0)
+    p.lse[(int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)n * p.l_ss] =
+        lsum > 0.f ? (Mu + fast_log2(lsum)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -558,6 +646,87 @@ static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStr
 
 template <int D>
 constexpr int fwd_bm() { return FwdCfg<D>::NW * 32 * FwdCfg<D>::RB; }
+
+template <int D>
+constexpr int fwd_bn() { return FwdCfg<D>::BN; }
+
+int fwd_block_n(int d) {
+  switch (d) {
+    case 32: return fwd_bn<32>();
+    case 64: return fwd_bn<64>();
+    case 96: return fwd_bn<96>();
+    case 128: return fwd_bn<128>();
+    default: return fwd_bn<256>();
+  }
+}
+
+#ifndef FAL_FWD_SPLIT
+#define FAL_FWD_SPLIT 1   // split the key range of grids smaller than the GPU
+#endif
+#ifndef FAL_FWD_SPLIT_MIN_TILES
+#define FAL_FWD_SPLIT_MIN_TILES 4   // key tiles per split, at least
+#endif
+
+// Split-KV plan.  Measured on MI355X (workgroup timestamps, head_dim 64): a workgroup
+// takes about 5 us of start-up and epilogue plus about 0.7 us per key tile, so a grid
+// with fewer workgroups than CUs ends with its longest chain of key tiles.  Splitting
+// the chain costs the partial outputs: fp32 rows written back to HBM when the kernel
+// ends (about 2.5 TB/s) and read again by the combine kernel, plus about 5 us for that
+// second launch.  A split is taken only when the chain time it saves exceeds that cost
+// (so C1, 2 x 8 heads x 1024 rows, stays whole: 16 tiles save 5.6 us at two splits but
+// cost 11.7 us), with the split count that saves the most.
+size_t fwd_split_plan(int64_t B, int64_t Hq, int64_t Nq, int64_t Nk, int d, int causal, int* kchunk, int* nsplit) {
+  *kchunk = 0;
+  *nsplit = 1;
+  if (!FAL_FWD_SPLIT || B <= 0 || Nq <= 0 || Nk <= 0) return 0;
+  const int64_t bm = fwd_block_m(d), bn = fwd_block_n(d);
+  const int64_t nwg = B * Hq * ((Nq + bm - 1) / bm);
+  const int64_t kspan = causal ? std::min<int64_t>(Nk, (Nq + bm - 1) / bm * bm) : Nk;
+  const int64_t maxtiles = (kspan + bn - 1) / bn;
+  if (nwg >= 256 || maxtiles < 2 * FAL_FWD_SPLIT_MIN_TILES) return 0;
+  const double us_per_tile = 0.7 * (d / 64.0 < 1.0 ? 1.0 : d / 64.0) * (bn / 64.0);
+  double best = 0.0;
+  for (int64_t ns = 2; ns <= 64 && nwg * ns <= 2048; ns *= 2) {
+    const int64_t chunk = std::max<int64_t>(FAL_FWD_SPLIT_MIN_TILES, (maxtiles + ns - 1) / ns);
+    const int64_t nsr = (maxtiles + chunk - 1) / chunk;
+    if (nsr < 2) break;
+    const double bytes = (double)(B * Hq * nsr * Nq) * (d + 2) * 4.0;
+    const double gain = us_per_tile * (double)(maxtiles - chunk) - 5.0 - 2.0 * bytes / 2.5e6;
+    if (gain > best && bytes <= (double)(size_t(256) << 20)) {
+      best = gain;
+      *kchunk = (int)chunk;
+      *nsplit = (int)nsr;
+    }
+  }
+  if (!*kchunk) return 0;
+  return (size_t)(B * Hq * *nsplit * Nq) * (size_t)(d + 2) * sizeof(float) + 256;
+}
+
+template <class T, int D>
+static hipError_t launch_combine_t(const FwdParams& p, int causal, hipStream_t st) {
+  constexpr int BM = FwdCfg<D>::NW * 32 * FwdCfg<D>::RB, BN = FwdCfg<D>::BN;
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Nq;
+  const dim3 grid((unsigned)((rows + 256 / (D / 8) - 1) / (256 / (D / 8))));
+  if (causal)
+    hipLaunchKernelGGL((fwd_combine_kernel<T, D, BM, BN, true>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((fwd_combine_kernel<T, D, BM, BN, false>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+template <int D>
+static hipError_t launch_combine_d(const FwdParams& p, int causal, hipStream_t st) {
+  return p.bf16 ? launch_combine_t<bf16_t, D>(p, causal, st) : launch_combine_t<half_t, D>(p, causal, st);
+}
+hipError_t launch_fwd_combine(const FwdParams& p, int d, int causal, hipStream_t st) {
+  switch (d) {
+    case 32: return launch_combine_d<32>(p, causal, st);
+    case 64: return launch_combine_d<64>(p, causal, st);
+    case 96: return launch_combine_d<96>(p, causal, st);
+    case 128: return launch_combine_d<128>(p, causal, st);
+    case 256: return launch_combine_d<256>(p, causal, st);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 int fwd_block_m(int d) {
   switch (d) {

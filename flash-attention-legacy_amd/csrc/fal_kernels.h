@@ -31,6 +31,14 @@ struct FwdParams {
   const int* cu_k;
   const int2* work;
   int bf16;           // element type of every fp16/bf16 tensor: 0 fp16, 1 bf16
+  // Batched split-KV (grids too small to fill the GPU): each query tile's key tiles
+  // are cut into splits of `kchunk` tiles, one workgroup each; the workgroups write
+  // unnormalised partial outputs and their (max, sum), and fwd_combine_kernel merges
+  // them.  kchunk = 0: one workgroup covers the whole key range and writes O and L.
+  int kchunk;
+  int nsplit;         // splits per query tile (grid = B * Hq * n_qtiles * nsplit)
+  float* part_o;      // [B * Hq * nsplit, Nq, d] fp32
+  float* part_ml;     // [B * Hq * nsplit, Nq, 2]: log2-domain max m and sum l (true sum 2^m * l)
 };
 
 // Backward.  Same addressing as FwdParams, plus dO (do_*), the fp32 dQ
@@ -98,6 +106,11 @@ struct DecodeParams {
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 int fwd_block_m(int d);
+int fwd_block_n(int d);
+// Split-KV plan for a batched forward: sets kchunk / nsplit (kchunk 0 = no split) and
+// returns the workspace bytes the split needs (0 without a split).
+size_t fwd_split_plan(int64_t B, int64_t Hq, int64_t Nq, int64_t Nk, int d, int causal, int* kchunk, int* nsplit);
+hipError_t launch_fwd_combine(const FwdParams& p, int d, int causal, hipStream_t st);
 // Rows of up to two packed [rows, heads, d] 16-bit tensors that the schedule kernel
 // zeroes: those before the first segment and from the end of the last one on
 // (the rows no segment covers when cu_seqlens is monotone).
@@ -120,6 +133,7 @@ int bwd_dq_block_m(int d);
 hipError_t launch_bwd_dq(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 
 int decode_chunk(int d, int B, int Hkv, int max_seqlen);
+
 hipError_t launch_decode(const DecodeParams& p, int d, hipStream_t st);
 
 }  // namespace fal

@@ -53,7 +53,8 @@ def _load() -> ctypes.CDLL:
         "fal_last_error": (ctypes.c_char_p, []),
         "fal_version": (ctypes.c_char_p, []),
         "fal_device_supported": (_INT, [_INT]),
-        "fal_fwd": (_INT, [_VP] * 5 + [_I64] * 6 + [_STR] * 4 + [_F32, _INT, _VP]),
+        "fal_fwd_workspace_size": (_SZ, [_I64] * 5 + [_INT]),
+        "fal_fwd": (_INT, [_VP] * 5 + [_I64] * 6 + [_STR] * 4 + [_F32, _INT, _VP, _SZ, _VP]),
         "fal_fwd_varlen_workspace_size": (_SZ, [_I64] * 4),
         "fal_fwd_varlen": (_INT, [_VP] * 7 + [_I64] * 8 + [_STR] * 4 + [_F32, _INT, _VP, _SZ, _VP]),
         "fal_bwd_workspace_size": (_SZ, [_I64] * 4),
@@ -78,7 +79,7 @@ _lib = _load()
 # Exported names, for introspection and tests.
 SYMBOLS = (
     "fal_last_error", "fal_version", "fal_device_supported",
-    "fal_fwd", "fal_fwd_varlen_workspace_size", "fal_fwd_varlen",
+    "fal_fwd_workspace_size", "fal_fwd", "fal_fwd_varlen_workspace_size", "fal_fwd_varlen",
     "fal_bwd_workspace_size", "fal_bwd", "fal_bwd_varlen_workspace_size", "fal_bwd_varlen",
     "fal_decode_workspace_size", "fal_decode",
     "fal_fwd_bf16", "fal_fwd_varlen_bf16", "fal_bwd_bf16", "fal_bwd_varlen_bf16", "fal_decode_bf16",
@@ -207,9 +208,14 @@ def forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, softmax_scale: fl
     L = torch.empty((B, Hq, N), dtype=torch.float32, device=dev)
     arr, (qs, ks, vs, os_) = _stride_block(Q, K, V, O)
     fwd = _fn("fal_fwd", Q.dtype)
+    causal = int(bool(is_causal))
+    # non-zero only for grids smaller than the GPU (split-KV partials)
+    nws = _lib.fal_fwd_workspace_size(B, Hq, N, Nk, d, causal)
+    ws = _workspace(nws, dev) if nws else None
     _check(_run(dev, lambda: fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), L.data_ptr(),
-                                 B, Hq, Hkv, N, Nk, d, qs, ks, vs, os_, float(softmax_scale),
-                                 int(bool(is_causal)), _raw_stream(dev.index))))
+                                 B, Hq, Hkv, N, Nk, d, qs, ks, vs, os_, float(softmax_scale), causal,
+                                 ws.data_ptr() if ws is not None else None, nws,
+                                 _raw_stream(dev.index))))
     return [O, L]
 
 

@@ -61,12 +61,20 @@ int fal_device_supported(int device);
  * Nq == Nk (flash_attn_legacy.cpp:58); Nq != Nk is accepted here with the same
  * top-left causal alignment (key j is visible to query i iff j <= i).
  */
+/* workspace: fal_fwd_workspace_size bytes.  It is 0 (workspace may be NULL) unless the
+ * grid is smaller than the GPU (fewer than 256 query tiles of 128 rows over batch and
+ * heads, with long key ranges): such calls split each query tile's key range over
+ * several workgroups, keep their partial outputs in the workspace and merge them in a
+ * second kernel (a "split-KV" forward).  The results are the same up to fp32 rounding. */
+size_t fal_fwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t seqlen_k,
+                              int64_t head_dim, int is_causal);
 int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
             int64_t batch, int64_t heads_q, int64_t heads_kv,
             int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
             const int64_t* q_strides, const int64_t* k_strides,
             const int64_t* v_strides, const int64_t* o_strides,
-            float softmax_scale, int is_causal, void* stream);
+            float softmax_scale, int is_causal,
+            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Forward attention over packed variable-length sequences.
@@ -173,7 +181,8 @@ int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* ls
                  int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
                  const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides,
-                 float softmax_scale, int is_causal, void* stream);
+                 float softmax_scale, int is_causal,
+                 void* workspace, size_t workspace_bytes, void* stream);
 int fal_fwd_varlen_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                         const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t num_seqs,
                         int64_t total_q, int64_t total_k, int64_t heads_q, int64_t heads_kv,

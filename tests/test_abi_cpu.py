@@ -60,7 +60,8 @@ def s3(*v):
 def fwd(lib, d=64, hq=4, hkv=2, ptr=4096, strides=None, lse=4096, bf16=False):
     st = strides or s3(4 * 16 * d, 16 * d, d)
     return (lib.fal_fwd_bf16 if bf16 else lib.fal_fwd)(ctypes.c_void_p(ptr), ctypes.c_void_p(ptr), ctypes.c_void_p(ptr), ctypes.c_void_p(ptr),
-                       ctypes.c_void_p(lse) if lse else None, 1, hq, hkv, 16, 16, d, st, st, st, st, 0.125, 1, None)
+                       ctypes.c_void_p(lse) if lse else None, 1, hq, hkv, 16, 16, d, st, st, st, st, 0.125, 1,
+                       None, 0, None)
 
 
 def test_forward_rejects_head_dim(lib):
@@ -92,6 +93,23 @@ def test_forward_rejects_null_misaligned_and_strides(lib):
     assert fwd(lib, strides=s3(1000, 100, 66)) == FAL_ERR_INVALID
     assert b"multiple of 8" in lib.fal_last_error()
     assert fwd(lib, lse=0) == FAL_ERR_INVALID
+
+
+def test_forward_split_workspace(lib):
+    """Grids far smaller than the GPU with long key ranges (one head of 16384 rows) split
+    the key range and need a workspace for the partial outputs; C1 (2 x 8 heads x 1024
+    rows, where the partials would cost more than the shorter chain saves) and C2 need
+    none, and neither do short key ranges."""
+    one = lib.fal_fwd_workspace_size(1, 1, 16384, 16384, 64, 1)
+    assert one >= 2 * 16384 * 66 * 4                  # at least two splits of every row
+    assert lib.fal_fwd_workspace_size(2, 8, 1024, 1024, 64, 1) == 0
+    assert lib.fal_fwd_workspace_size(4, 32, 4096, 4096, 128, 1) == 0
+    assert lib.fal_fwd_workspace_size(2, 8, 128, 128, 64, 1) == 0
+    st = s3(16384 * 64, 16384 * 64, 64)
+    p = ctypes.c_void_p(4096)
+    rc = lib.fal_fwd(p, p, p, p, p, 1, 1, 1, 16384, 16384, 64, st, st, st, st, 0.125, 1, None, 0, None)
+    assert rc == FAL_ERR_WORKSPACE
+    assert b"workspace needs" in lib.fal_last_error()
 
 
 def test_workspace_sizes_and_checks(lib):
@@ -126,7 +144,7 @@ def test_error_message_cleared_on_success(lib, ext):
     # batch == 0 is a valid no-op (no GPU work is enqueued)
     st = s3(0, 0, 64)
     p = ctypes.c_void_p(4096)
-    assert lib.fal_fwd(p, p, p, p, p, 0, 4, 2, 16, 16, 64, st, st, st, st, 0.125, 0, None) == FAL_OK
+    assert lib.fal_fwd(p, p, p, p, p, 0, 4, 2, 16, 16, 64, st, st, st, st, 0.125, 0, None, 0, None) == FAL_OK
     assert lib.fal_last_error() == b""
 
 

@@ -142,3 +142,25 @@ def test_cache_seqlens_beyond_capacity_are_clamped():
     o_g, l_g = run(q, kc, vc, [S, 5, 0], 0.088, lse=True)
     o_b, l_b = run(q, kc, vc, [S + 1000, 5, -3], 0.088, lse=True)
     assert torch.equal(o_g, o_b) and torch.equal(l_g, l_b)
+
+
+@pytest.mark.parametrize("B", [1, 63, 64, 65, 130])
+def test_decode_batch_sizes_both_schedules(B):
+    """Batches of up to 64 sequences derive their (sequence, split) items inside the
+    split kernel; larger batches take the schedule kernel's list.  Both against the
+    oracle, with lengths that give full splits, partial last splits and empty rows."""
+    g = torch.Generator().manual_seed(B)
+    hq, hkv, d = 8, 2, 64
+    lens = [int(x) for x in torch.randint(0, 5000, (B,), generator=g)]
+    lens[0] = 4096                       # an exact multiple of the split size
+    if B > 2:
+        lens[1], lens[2] = 0, 1
+    S = max(lens)
+    q = randn((B, hq, d), seed=70)
+    kc, vc = randn((B, S, hkv, d), seed=71), randn((B, S, hkv, d), seed=72)
+    o, lse = run(q, kc, vc, lens, 0.125, lse=True)
+    ro, rl = ref(q, kc, vc, lens, 0.125)
+    assert max_abs(o, ro) <= FWD_ATOL
+    fin = torch.isfinite(rl)
+    assert torch.equal(torch.isfinite(lse.cpu()), fin)
+    assert max_abs(lse.cpu()[fin], rl[fin]) <= 1e-3
