@@ -13,8 +13,10 @@ one JSON object:
   average launch time (HIP events on the launch stream, same timed region),
   against the 2.5 PFLOP/s dense fp16 MFMA peak; ``traffic`` comes from the
   committed rocprofv3 counter summary when present;
-* ``prerun_s``: seconds of untimed C2 calls before the warmup, so the timed steps
-  run at the clock the GPU holds under sustained load;
+* ``prerun_s``: seconds of untimed calls of the workload right before its warmup
+  (a quarter of it for each extra workload), so the timed steps run at the clock the
+  GPU holds under sustained load rather than in the ramp after the host-side input
+  creation left it idle;
 * ``cpu_baseline``: fp32 PyTorch attention (the reference's own test formula) on
   this host's CPU cores over a bounded sample of the same workload;
 * ``extra``: the other configurations measured the same way -- C1 forward, C3
@@ -53,10 +55,25 @@ def fwd_flops(b, hq, nq, nk, d, causal):
     return f / 2 if causal else f
 
 
-def time_steps(fn, steps, warmup):
-    """Run `fn` warmup times, then time `steps` calls.  Returns (wall ms/step,
-    event ms/step) -- the events are recorded on the current stream, which is the
-    stream the kernels are launched on."""
+PRERUN_S = 0.0   # seconds of untimed calls before each workload's warmup (set from --prerun-s)
+
+
+def settle(fn, seconds):
+    """Call `fn` back to back for `seconds` of wall time, untimed.  After the host has
+    kept the GPU idle (creating inputs), its first launches run up to ~30% slower while
+    clocks and power ramp back; this brings every timed region to the steady state."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_steps(fn, steps, warmup, prerun=None):
+    """Run `fn` for the pre-run time, `warmup` more times, then time `steps` calls.
+    Returns (wall ms/step, event ms/step) -- the events are recorded on the current
+    stream, which is the stream the kernels are launched on."""
+    settle(fn, PRERUN_S if prerun is None else prerun)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -209,23 +226,6 @@ def cpu_baseline(budget_s=15.0):
                       f"causal), fp32 torch on CPU, {dt:.1f} s; threads={threads}, os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
 
 
-def prerun(seconds):
-    """C2 forward calls for a fixed wall time before the warmup and the timed steps: the
-    GPU's clock settles under sustained MFMA load (the first launches on an idle GPU run
-    slower).  Reported in the line as ``prerun_s``; none of it is timed."""
-    from flash_attn_legacy import hip_ext
-    if seconds <= 0:
-        return 0.0
-    B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
-    q, k, v = randn((B, Hq, N, d), 10), randn((B, Hkv, N, d), 11), randn((B, Hkv, N, d), 12)
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(10):
-            hip_ext.forward(q, k, v, 0.088, True)
-        torch.cuda.synchronize()
-    return round(time.perf_counter() - t0, 2)
-
-
 def load_traffic():
     """HBM bytes per C2 forward launch from the committed rocprofv3 counter summary."""
     path = os.path.join(ROOT, "profiles", "fwd_c2_traffic.json")
@@ -243,7 +243,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--prerun-s", type=float, default=2.0,
-                    help="seconds of untimed C2 forward calls before the warmup (clock settling)")
+                    help="seconds of untimed calls of the workload right before its warmup (clock "
+                         "settling); the extra workloads get a quarter of it each")
     ap.add_argument("--only", choices=["c2", "all", "copy"], default="all",
                     help="c2: the headline line without the extra configurations; copy: a 1 GiB "
                          "device copy only, the known-size kernel that calibrates HBM byte counters")
@@ -264,10 +265,13 @@ def main():
                           "gbs": round(2 * src.numel() * 2 / ev / 1e6, 1)}), flush=True)
         return
 
-    pre_s = prerun(a.prerun_s)
+    global PRERUN_S
+    PRERUN_S = max(a.prerun_s, 0.0)
     wall, ev, flops = bench_c2(a.steps, a.warmup)
     value = flops / (wall * 1e-3) / 1e12
     achieved = flops / (ev * 1e-3) / 1e12
+    # the other workloads: a quarter of the pre-run each (they are short)
+    PRERUN_S = PRERUN_S / 4
     extra = bench_extra(max(5, a.steps // 2), max(2, a.warmup // 2)) if a.only == "all" else {}
     if a.only == "all":
         extra["varlen_vs_padded"] = bench_varlen_vs_padded(max(5, a.steps // 2), max(2, a.warmup // 2))
@@ -279,7 +283,7 @@ def main():
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "prerun_s": pre_s,
+        "prerun_s": max(a.prerun_s, 0.0),
         "ms_per_step": round(wall, 4),
         "higher_is_better": True,
         "scaling": "weak",

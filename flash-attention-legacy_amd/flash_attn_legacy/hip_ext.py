@@ -119,6 +119,17 @@ def _stride_block(*ts: torch.Tensor):
     return arr, [ctypes.byref(arr, 24 * i) for i in range(len(ts))]
 
 
+def _packed_block(*ts: torch.Tensor):
+    """The (unused, head, token) strides of packed [total, H, d] tensors in one ctypes
+    array, and a pointer to each tensor's triple."""
+    vals = []
+    for t in ts:
+        s = t.stride()
+        vals.extend((0, s[1], s[0]))
+    arr = (ctypes.c_int64 * len(vals))(*vals)
+    return arr, [ctypes.byref(arr, 24 * i) for i in range(len(ts))]
+
+
 try:
     _raw_stream = torch._C._cuda_getCurrentRawStream   # the current stream's hipStream_t as an int
 except AttributeError:   # pragma: no cover - older torch
@@ -245,17 +256,21 @@ def forward_varlen(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_s
     if cu_seqlens_k.shape[0] != num_seqs + 1:
         raise RuntimeError("cu_seqlens_k length mismatch")
     Q, K, V = _usable(Q), _usable(K), _usable(V)
-    cu_q = cu_seqlens_q.to(Q.device).contiguous()
-    cu_k = cu_seqlens_k.to(Q.device).contiguous()
-    O = torch.empty((total_q, Hq, d), dtype=Q.dtype, device=Q.device)
-    L = torch.empty((total_q, Hq), dtype=torch.float32, device=Q.device)
-    ws = _workspace(_lib.fal_fwd_varlen_workspace_size(num_seqs, total_q, int(max_seqlen_q), d), Q.device)
-    with torch.cuda.device(Q.device):
-        _check(_fn("fal_fwd_varlen", Q.dtype)(
-            _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(L), _ptr(cu_q), _ptr(cu_k),
-            num_seqs, total_q, total_k, Hq, Hkv, d, int(max_seqlen_q), int(max_seqlen_k),
-            _strides(Q, (None, 1, 0)), _strides(K, (None, 1, 0)), _strides(V, (None, 1, 0)), _strides(O, (None, 1, 0)),
-            float(softmax_scale), int(bool(is_causal)), _ptr(ws), ws.numel(), _stream(Q.device)))
+    dev = Q.device
+    cu_q = cu_seqlens_q if cu_seqlens_q.device == dev and cu_seqlens_q.is_contiguous() else \
+        cu_seqlens_q.to(dev).contiguous()
+    cu_k = cu_seqlens_k if cu_seqlens_k.device == dev and cu_seqlens_k.is_contiguous() else \
+        cu_seqlens_k.to(dev).contiguous()
+    O = torch.empty((total_q, Hq, d), dtype=Q.dtype, device=dev)
+    L = torch.empty((total_q, Hq), dtype=torch.float32, device=dev)
+    nws = _lib.fal_fwd_varlen_workspace_size(num_seqs, total_q, int(max_seqlen_q), d)
+    ws = _workspace(nws, dev)
+    arr, (qs, ks, vs, os_) = _packed_block(Q, K, V, O)
+    fwd = _fn("fal_fwd_varlen", Q.dtype)
+    _check(_run(dev, lambda: fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), L.data_ptr(),
+                                 cu_q.data_ptr(), cu_k.data_ptr(), num_seqs, total_q, total_k, Hq, Hkv, d,
+                                 int(max_seqlen_q), int(max_seqlen_k), qs, ks, vs, os_, float(softmax_scale),
+                                 int(bool(is_causal)), ws.data_ptr(), nws, _raw_stream(dev.index))))
     return [O, L]
 
 
