@@ -154,11 +154,38 @@ VARLEN_SCENARIOS = [
 ]
 
 
+def graph_ms(fn, calls=20, replays=5):
+    """GPU time per call without the host's per-call overhead: `calls` calls captured in
+    one HIP graph, replayed `replays` times between events (after one untimed replay)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (calls * replays)
+
+
 def bench_varlen_vs_padded(steps, warmup):
     """Padded batch (every sequence padded to the longest, ``flash_attention``) against
     the packed batch (``flash_attn_varlen_func``) through the public API, as the
     reference's benchmark does; plus the same comparison on C4's lengths (16 sequences
-    U[64, 4096], 32/8 heads, d=128), where the padded batch is [16, H, 4096, 128]."""
+    U[64, 4096], 32/8 heads, d=128), where the padded batch is [16, H, 4096, 128].
+    *_ms are per call through the API (host overhead included: the small scenarios are
+    host-bound); *_gpu_ms are the same calls replayed from a captured HIP graph."""
     from flash_attn_legacy import flash_attention, flash_attn_varlen_func
     out = {}
 
@@ -168,16 +195,19 @@ def bench_varlen_vs_padded(steps, warmup):
         qp, kp, vp = randn((B, hq, mx, d), seed), randn((B, hkv, mx, d), seed + 1), randn((B, hkv, mx, d), seed + 2)
         qv, kv, vv = randn((tot, hq, d), seed), randn((tot, hkv, d), seed + 1), randn((tot, hkv, d), seed + 2)
         cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32, device="cuda")
+        pad = lambda: flash_attention(qp, kp, vp, softmax_scale=scale, is_causal=True)
+        pack = lambda: flash_attn_varlen_func(qv, kv, vv, cu, cu, mx, mx, softmax_scale=scale, causal=True)
         with torch.no_grad():
-            _, pad_ms = time_steps(lambda: flash_attention(qp, kp, vp, softmax_scale=scale, is_causal=True),
-                                   steps, warmup)
-            _, pack_ms = time_steps(lambda: flash_attn_varlen_func(qv, kv, vv, cu, cu, mx, mx, softmax_scale=scale,
-                                                                   causal=True), steps, warmup)
+            _, pad_ms = time_steps(pad, steps, warmup)
+            _, pack_ms = time_steps(pack, steps, warmup)
+            pad_gpu, pack_gpu = graph_ms(pad), graph_ms(pack)
         useful = sum(fwd_flops(1, hq, n, n, d, True) for n in lens)
         out[name] = {"seqs": B, "max_len": mx, "tokens": tot,
                      "padding_waste": round(1 - tot / (B * mx), 3),
                      "padded_ms": round(pad_ms, 4), "packed_ms": round(pack_ms, 4),
                      "speedup": round(pad_ms / pack_ms, 2),
+                     "padded_gpu_ms": round(pad_gpu, 4), "packed_gpu_ms": round(pack_gpu, 4),
+                     "gpu_speedup": round(pad_gpu / pack_gpu, 2),
                      "packed_useful_tflops": round(useful / pack_ms / 1e9, 1)}
 
     for i, (name, lens) in enumerate(VARLEN_SCENARIOS):

@@ -176,6 +176,7 @@ int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* ls
 
 size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q, int64_t head_dim) {
   (void)max_seqlen_q;
+  if (num_seqs <= kVarlenSmallSeqs) return 0;   // the kernel derives its work items itself
   const int bm = fwd_block_m(head_dim_ok(head_dim) ? (int)head_dim : 128);
   const int64_t cap = (total_q + bm - 1) / bm + num_seqs;
   return align256((size_t)cap * sizeof(int2));
@@ -212,20 +213,24 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
     return rc;
   if (!lse) return fail(FAL_ERR_INVALID, "lse: null pointer");
   const size_t need = fal_fwd_varlen_workspace_size(num_seqs, total_q, max_seqlen_q, head_dim);
-  if (!workspace || workspace_bytes < need)
+  if (need && (!workspace || workspace_bytes < need))
     return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
   if (num_seqs == 0 || total_q == 0) return ok();
 
   const int bm = fwd_block_m((int)head_dim);
   const int cap = (int)((total_q + bm - 1) / bm + num_seqs);
-  int2* work = static_cast<int2*>(workspace);
-  int nb = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
-  nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // grouped by sequence (see varlen_schedule_kernel): K/V locality in each XCD's L2
-  hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nb, FAL_FWD_VARLEN_ORDER,
-                                        work, cap, st);
-  if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
+  int2* work = nullptr;
+  if (need) {
+    // grouped by sequence (see varlen_schedule_kernel): K/V locality in each XCD's L2;
+    // smaller batches derive the same order inside the forward kernel
+    work = static_cast<int2*>(workspace);
+    int nb = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
+    nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
+    hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nb,
+                                          FAL_FWD_VARLEN_ORDER, work, cap, st);
+    if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
+  }
 
   FwdParams p{};
   p.bf16 = bf16;
@@ -246,7 +251,8 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
   p.total_k = (int)total_k;
   p.cu_k = cu_seqlens_k;
   p.work = work;
-  p.n_qtiles = cap;   // work-list capacity
+  p.num_seqs = (int)num_seqs;
+  p.n_qtiles = cap;   // work-list capacity (an upper bound on the item count)
   const int64_t groups8 = ((int64_t)cap * heads_kv + 7) / 8 * 8;
   const int64_t nblocks = groups8 * (heads_q / heads_kv);
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");

@@ -48,9 +48,40 @@ struct FwdItem {
   int b, hq, qt, q_off, k_off, nq, nk, split;
 };
 
-// Resolves the work item of this workgroup; false for a padding block, which exits.
+// Item `item` of the varlen forward work list for at most 64 sequences, derived in the
+// wave from cu_seqlens (no schedule kernel): the same order as the grouped list of
+// varlen_schedule_kernel, i.e. sequences by tile count, most tiles first (ties by
+// index), each sequence's tiles contiguous, its last (heaviest causal) tile first.
+// Lane s holds sequence s; every wave of the workgroup computes the same result.
+// False past the end of the list.
+__device__ __forceinline__ bool varlen_item_small(const int* cu, int num_seqs, int total, int tile, int item,
+                                                  int& seq, int& qtile) {
+  const int lane = threadIdx.x & 63;
+  int nt = 0;
+  if (lane < num_seqs) {
+    int off, len;
+    seg_bounds(cu, lane, total, off, len);
+    nt = cdiv(len, tile);
+  }
+  // first list index of this lane's sequence: the tiles of every sequence ordered before it
+  int start = 0;
+  for (int s = 0; s < num_seqs; ++s) {
+    const int ns = __builtin_amdgcn_readlane(nt, s);
+    start += (ns > nt || (ns == nt && s < lane)) ? ns : 0;
+  }
+  const bool mine = lane < num_seqs && item >= start && item < start + nt;
+  const uint64_t m = __builtin_amdgcn_ballot_w64(mine);
+  if (!m) return false;
+  const int src = __builtin_ctzll(m);
+  seq = src;
+  qtile = __builtin_amdgcn_readlane(nt, src) - 1 - (item - __builtin_amdgcn_readlane(start, src));
+  return true;
+}
+
+// Resolves the work item of this workgroup (query tiles of `bm` rows); false for a
+// padding block, which exits.
 template <bool CAUSAL>
-__device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
+__device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm) {
   if (p.cu_q) {
     // 1-D grid over (work item, KV head) groups of G query heads.  Block i runs on XCD
     // i % 8 as that XCD's (i / 8)-th block; the groups are dealt to the XCDs round-robin
@@ -62,14 +93,21 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it) {
     const int grp = (k8 / g) * 8 + (blockIdx.x & 7);
     const int item = grp / p.Hkv;
     if (item >= p.n_qtiles) return false;
-    const int2 wk = p.work[item];
-    if (wk.x < 0) return false;
+    int seq, qt;
+    if (p.work) {
+      const int2 wk = p.work[item];
+      seq = wk.x;
+      qt = wk.y;
+      if (seq < 0) return false;
+    } else if (!varlen_item_small(p.cu_q, p.num_seqs, p.total_q, bm, item, seq, qt)) {
+      return false;
+    }
     it.hq = (grp % p.Hkv) * g + k8 % g;
     it.b = 0;
     it.split = 0;
-    it.qt = wk.y;
-    seg_bounds(p.cu_q, wk.x, p.total_q, it.q_off, it.nq);
-    seg_bounds(p.cu_k, wk.x, p.total_k, it.k_off, it.nk);
+    it.qt = qt;
+    seg_bounds(p.cu_q, seq, p.total_q, it.q_off, it.nq);
+    seg_bounds(p.cu_k, seq, p.total_k, it.k_off, it.nk);
   } else {
     // 1-D grid; group heads of one KV head and the query tiles of a head together so the
     // workgroups an XCD runs at once share K/V in that XCD's L2 (workgroups are dealt to
@@ -125,7 +163,7 @@ fwd_kernel(FwdParams p) {
 
   // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
   FwdItem it;
-  if (!fwd_item<CAUSAL>(p, it)) return;
+  if (!fwd_item<CAUSAL>(p, it, BM)) return;
   const int b = it.b, hq = it.hq, qt = it.qt, q_off = it.q_off, k_off = it.k_off, nq = it.nq, nk = it.nk;
   const int hkv = hq / (p.Hq / p.Hkv);
   const int m0 = qt * BM;

@@ -29,7 +29,8 @@ struct FwdParams {
   float scale_log2;   // softmax_scale * log2(e), signed, |.| >= 1e-30
   const int* cu_q;
   const int* cu_k;
-  const int2* work;
+  const int2* work;   // varlen work list; null: each workgroup derives its item from cu_q
+  int num_seqs;       // varlen: segments in cu_q / cu_k (used when work is null)
   int bf16;           // element type of every fp16/bf16 tensor: 0 fp16, 1 bf16
   // Batched split-KV (grids too small to fill the GPU): each query tile's key tiles
   // are cut into splits of `kchunk` tiles, one workgroup each; the workgroups write
@@ -120,6 +121,9 @@ struct ZeroRows {
   int64_t a_row, a_head, b_row, b_head;   // element strides
   int heads, d;
 };
+// Varlen batches of at most this many sequences need no schedule kernel: each forward
+// workgroup derives its (sequence, tile) item from cu_seqlens itself.
+constexpr int kVarlenSmallSeqs = 64;
 hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int rows, int tile, int nbuckets, int descending,
                                   int2* work, int capacity, hipStream_t st, const ZeroRows* zero = nullptr);
 

@@ -263,14 +263,16 @@ def forward_varlen(Q, K, V, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, max_s
         cu_seqlens_k.to(dev).contiguous()
     O = torch.empty((total_q, Hq, d), dtype=Q.dtype, device=dev)
     L = torch.empty((total_q, Hq), dtype=torch.float32, device=dev)
+    # zero for up to 64 sequences (the kernel derives its work items from cu_seqlens)
     nws = _lib.fal_fwd_varlen_workspace_size(num_seqs, total_q, int(max_seqlen_q), d)
-    ws = _workspace(nws, dev)
+    ws = _workspace(nws, dev) if nws else None
     arr, (qs, ks, vs, os_) = _packed_block(Q, K, V, O)
     fwd = _fn("fal_fwd_varlen", Q.dtype)
     _check(_run(dev, lambda: fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), L.data_ptr(),
                                  cu_q.data_ptr(), cu_k.data_ptr(), num_seqs, total_q, total_k, Hq, Hkv, d,
                                  int(max_seqlen_q), int(max_seqlen_k), qs, ks, vs, os_, float(softmax_scale),
-                                 int(bool(is_causal)), ws.data_ptr(), nws, _raw_stream(dev.index))))
+                                 int(bool(is_causal)), ws.data_ptr() if ws is not None else None, nws,
+                                 _raw_stream(dev.index))))
     return [O, L]
 
 

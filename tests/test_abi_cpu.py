@@ -119,12 +119,15 @@ def test_workspace_sizes_and_checks(lib):
     for d in (32, 64, 96, 128):
         assert rows * 4 <= lib.fal_bwd_workspace_size(2, 16, 2048, d) < rows * 4 + 4096
     assert lib.fal_bwd_workspace_size(2, 16, 2048, 256) >= rows * 257 * 4
-    assert lib.fal_fwd_varlen_workspace_size(16, 35901, 4096, 128) >= (35901 // 128 + 16) * 8
+    # up to 64 sequences the forward derives its work items in the kernel: no workspace
+    assert lib.fal_fwd_varlen_workspace_size(16, 35901, 4096, 128) == 0
+    assert lib.fal_fwd_varlen_workspace_size(64, 35901, 4096, 128) == 0
+    assert lib.fal_fwd_varlen_workspace_size(65, 35901, 4096, 128) >= (35901 // 128 + 65) * 8
     assert lib.fal_decode_workspace_size(32, 32, 8, 32768, 128) > 0
     st = s3(0, 64, 256)
     cu = ctypes.c_void_p(4096)
     p = ctypes.c_void_p(4096)
-    rc = lib.fal_fwd_varlen(p, p, p, p, p, cu, cu, 2, 64, 64, 4, 4, 64, 32, 32, st, st, st, st, 0.1, 1,
+    rc = lib.fal_fwd_varlen(p, p, p, p, p, cu, cu, 100, 6400, 6400, 4, 4, 64, 64, 64, st, st, st, st, 0.1, 1,
                             p, 8, None)
     assert rc == FAL_ERR_WORKSPACE
     assert b"workspace needs" in lib.fal_last_error()

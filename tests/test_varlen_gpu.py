@@ -73,6 +73,20 @@ def test_unequal_q_k_segments(causal):
     fwd_check([10, 70, 130], [140, 33, 130], 4, 2, 128, causal)
 
 
+@pytest.mark.parametrize("nseq", [63, 64, 65, 130])
+@pytest.mark.parametrize("causal", [False, True])
+def test_work_items_on_both_sides_of_64_sequences(nseq, causal):
+    """Up to 64 sequences each forward workgroup derives its (sequence, tile) item from
+    cu_seqlens; more use the schedule kernel's list.  Lengths repeat (equal tile counts
+    are ordered by index) and include empty segments and segments of several tiles."""
+    g = torch.Generator().manual_seed(nseq)
+    lens = [int(x) for x in torch.randint(0, 40, (nseq,), generator=g)]
+    lens[::7] = [0] * len(lens[::7])
+    lens[3] = 300
+    lens[nseq // 2] = 257
+    fwd_check(lens, lens, 2, 1, 64, causal, seed=nseq)
+
+
 def bwd_check(lens_q, lens_k, hq, hkv, d, causal, seed=0):
     tq, tk = sum(lens_q), sum(lens_k)
     q = randn((tq, hq, d), seed=seed)
