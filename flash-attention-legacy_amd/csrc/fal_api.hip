@@ -176,7 +176,8 @@ int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* ls
 
 size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q, int64_t head_dim) {
   (void)max_seqlen_q;
-  if (num_seqs <= kVarlenSmallSeqs) return 0;   // the kernel derives its work items itself
+  // small problems: the kernel derives its work items itself
+  if (num_seqs <= kVarlenSmallSeqs && total_q <= kVarlenSmallTokens) return 0;
   const int bm = fwd_block_m(head_dim_ok(head_dim) ? (int)head_dim : 128);
   const int64_t cap = (total_q + bm - 1) / bm + num_seqs;
   return align256((size_t)cap * sizeof(int2));

@@ -121,9 +121,18 @@ struct ZeroRows {
   int64_t a_row, a_head, b_row, b_head;   // element strides
   int heads, d;
 };
-// Varlen batches of at most this many sequences need no schedule kernel: each forward
-// workgroup derives its (sequence, tile) item from cu_seqlens itself.
-constexpr int kVarlenSmallSeqs = 64;
+// Small varlen forwards (at most this many sequences and query tokens) need no
+// schedule kernel: each workgroup derives its (sequence, tile) item from cu_seqlens
+// itself.  That saves a launch where launches dominate, and costs about 1% on large
+// batches (C4: 874 against 882 TFLOP/s), which keep the list.
+#ifndef FAL_VARLEN_SMALL_SEQS
+#define FAL_VARLEN_SMALL_SEQS 64
+#endif
+#ifndef FAL_VARLEN_SMALL_TOKENS
+#define FAL_VARLEN_SMALL_TOKENS 16384
+#endif
+constexpr int kVarlenSmallSeqs = FAL_VARLEN_SMALL_SEQS;
+constexpr int kVarlenSmallTokens = FAL_VARLEN_SMALL_TOKENS;
 hipError_t launch_varlen_schedule(const int* cu, int num_seqs, int rows, int tile, int nbuckets, int descending,
                                   int2* work, int capacity, hipStream_t st, const ZeroRows* zero = nullptr);
 

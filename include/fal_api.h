@@ -83,9 +83,9 @@ int fal_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
  *   lse [total_q, Hq] fp32 contiguous;
  *   cu_seqlens_q / cu_seqlens_k: device int32 [num_seqs + 1] prefix offsets.
  * max_seqlen_q bounds the longest query segment (used to size the on-device
- * tile schedule).  No host synchronisation: for more than 64 sequences the
- * (sequence, tile) work list is built on the device in `workspace`
- * (fal_fwd_varlen_workspace_size bytes); for up to 64 sequences the size is 0,
+ * tile schedule).  No host synchronisation: the (sequence, tile) work list is
+ * built on the device in `workspace` (fal_fwd_varlen_workspace_size bytes).  For
+ * small problems (up to 64 sequences and 16384 query tokens) the size is 0,
  * `workspace` may be null, and each workgroup derives its item from cu_seqlens_q.
  */
 size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q,

@@ -119,10 +119,12 @@ def test_workspace_sizes_and_checks(lib):
     for d in (32, 64, 96, 128):
         assert rows * 4 <= lib.fal_bwd_workspace_size(2, 16, 2048, d) < rows * 4 + 4096
     assert lib.fal_bwd_workspace_size(2, 16, 2048, 256) >= rows * 257 * 4
-    # up to 64 sequences the forward derives its work items in the kernel: no workspace
-    assert lib.fal_fwd_varlen_workspace_size(16, 35901, 4096, 128) == 0
-    assert lib.fal_fwd_varlen_workspace_size(64, 35901, 4096, 128) == 0
-    assert lib.fal_fwd_varlen_workspace_size(65, 35901, 4096, 128) >= (35901 // 128 + 65) * 8
+    # small problems (<= 64 sequences, <= 16384 query tokens) derive their work items in
+    # the kernel: no workspace; larger ones get a (sequence, tile) list
+    assert lib.fal_fwd_varlen_workspace_size(16, 1504, 1024, 64) == 0
+    assert lib.fal_fwd_varlen_workspace_size(64, 16384, 4096, 128) == 0
+    assert lib.fal_fwd_varlen_workspace_size(65, 6400, 256, 128) >= (6400 // 256 + 65) * 8
+    assert lib.fal_fwd_varlen_workspace_size(16, 35901, 4096, 128) >= (35901 // 256 + 16) * 8
     assert lib.fal_decode_workspace_size(32, 32, 8, 32768, 128) > 0
     st = s3(0, 64, 256)
     cu = ctypes.c_void_p(4096)

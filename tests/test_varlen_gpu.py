@@ -76,9 +76,10 @@ def test_unequal_q_k_segments(causal):
 @pytest.mark.parametrize("nseq", [63, 64, 65, 130])
 @pytest.mark.parametrize("causal", [False, True])
 def test_work_items_on_both_sides_of_64_sequences(nseq, causal):
-    """Up to 64 sequences each forward workgroup derives its (sequence, tile) item from
-    cu_seqlens; more use the schedule kernel's list.  Lengths repeat (equal tile counts
-    are ordered by index) and include empty segments and segments of several tiles."""
+    """Up to 64 sequences (and 16384 query tokens) each forward workgroup derives its
+    (sequence, tile) item from cu_seqlens; more use the schedule kernel's list.  Lengths
+    repeat (equal tile counts are ordered by index) and include empty segments and
+    segments of several tiles."""
     g = torch.Generator().manual_seed(nseq)
     lens = [int(x) for x in torch.randint(0, 40, (nseq,), generator=g)]
     lens[::7] = [0] * len(lens[::7])
