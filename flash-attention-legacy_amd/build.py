@@ -60,6 +60,13 @@ def _compile(src: str, verbose: bool, objdir: str = OBJ, defines=()) -> str:
 def build(jobs: int | None = None, verbose: bool = False, out: str = OUT, defines=()) -> str:
     """Compile and link; returns the path of the shared library.  `defines` are extra
     NAME=VALUE macros (kernel tunables); `out` is the library path to write."""
+    # the pipelined forward loop is generated text (csrc/gen_fwd_pipe.py)
+    sys.path.insert(0, CSRC)
+    try:
+        import gen_fwd_pipe
+        gen_fwd_pipe.main()
+    finally:
+        sys.path.remove(CSRC)
     objdir = OBJ if not defines else os.path.join(OBJ, "_".join(defines).replace("=", "-"))
     os.makedirs(objdir, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))

@@ -178,7 +178,7 @@ size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
   (void)max_seqlen_q;
   // small problems: the kernel derives its work items itself
   if (num_seqs <= kVarlenSmallSeqs && total_q <= kVarlenSmallTokens) return 0;
-  const int bm = fwd_block_m(head_dim_ok(head_dim) ? (int)head_dim : 128);
+  const int bm = fwd_block_m_varlen(head_dim_ok(head_dim) ? (int)head_dim : 128);
   const int64_t cap = (total_q + bm - 1) / bm + num_seqs;
   return align256((size_t)cap * sizeof(int2));
 }
@@ -218,7 +218,7 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
     return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
   if (num_seqs == 0 || total_q == 0) return ok();
 
-  const int bm = fwd_block_m((int)head_dim);
+  const int bm = fwd_block_m_varlen((int)head_dim);
   const int cap = (int)((total_q + bm - 1) / bm + num_seqs);
   hipStream_t st = static_cast<hipStream_t>(stream);
   int2* work = nullptr;

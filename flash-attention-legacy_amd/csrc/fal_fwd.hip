@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "fal_kernels.h"
+#include "fal_fwd_pipe.inc"
 
 namespace fal {
 
@@ -41,6 +42,9 @@ namespace fal {
 #endif
 #ifndef FAL_FWD_KDEPTH
 #define FAL_FWD_KDEPTH 2
+#endif
+#ifndef FAL_FWD_PIPE
+#define FAL_FWD_PIPE 1   // head_dim 128 at two row blocks per wave: software-pipelined tile loop
 #endif
 
 // A workgroup's (batch or sequence, query head, query tile) and its row ranges.
@@ -144,6 +148,10 @@ fwd_kernel(FwdParams p) {
   // instead pre-multiplies an fp16 Q by scale*log2(e), rounded once to fp16: that saves
   // the FMA but shifts large scores by up to ~1e-2 in log2 units, so it is off.
   constexpr bool PRESCALE = FAL_PRESCALE_FP16 && std::is_same<T, half_t>::value;
+  // PIPE: the key-tile loop is the software-pipelined asm block (head_dim 128, 64 query
+  // rows per wave, one wave per SIMD) with a ring of 4 K/V tiles copied two tiles ahead.
+  constexpr bool PIPE = FAL_FWD_PIPE && D == 128 && RB == 2 && NW == 4 && BN == 64 && !FAL_PRESCALE_FP16;
+  constexpr bool PIPE_SIGN = PIPE;
   constexpr int BM = NW * 32 * RB;  // query rows per workgroup (RB 32-row blocks per wave)
   constexpr int KS = D / 16;        // MFMA k-steps over the head dim
   constexpr int NKB = BN / 32;      // 32-key blocks per tile
@@ -153,7 +161,8 @@ fwd_kernel(FwdParams p) {
   constexpr int IPT = BN * CPR / (NW * 64);   // direct-to-LDS loads per wave per part
   static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(1024))) T smem[2 * 2 * PART];
+  constexpr int NSLOT = PIPE ? 4 : 2;
+  __shared__ __attribute__((aligned(1024))) T smem[NSLOT * 2 * PART];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -179,7 +188,10 @@ fwd_kernel(FwdParams p) {
   // Row block rb of wave w covers rows m0 + (w*RB + rb)*32 ..; each K or V fragment read
   // from LDS feeds RB MFMAs.  c = softmax_scale * log2(e), the sign included, takes
   // the scores to the log2 domain.
-  const float c = p.scale_log2;
+  // The pipelined loop masks raw scores with -inf, which needs c > 0: a negative scale
+  // is folded into Q (exact) and a zero scale becomes 1e-30 (every exponent rounds to 0).
+  const bool negq = PIPE_SIGN && p.scale_log2 < 0.f;
+  const float c = PIPE_SIGN ? fmaxf(fabsf(p.scale_log2), 1e-30f) : p.scale_log2;
   int row[RB];
   V8 qreg[RB][KS];
 #pragma unroll
@@ -191,6 +203,10 @@ fwd_kernel(FwdParams p) {
       if (PRESCALE) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = (T)((float)x[e] * c);
+      }
+      if (negq) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = -x[e];
       }
       qreg[rb][t] = x;
     }
@@ -408,6 +424,72 @@ fwd_kernel(FwdParams p) {
     tile_body(masked, j, buf);
   };
 
+  const int wrow_hi = m0 + (w * RB + RB - 1) * 32 + 31;   // last query row of this wave
+  if constexpr (PIPE) {
+    // The whole key-tile loop is one software-pipelined asm block (fal_fwd_pipe.inc,
+    // generated by gen_fwd_pipe.py): a 4-slot K/V ring copied two tiles ahead, PV of
+    // tile j-1 and S of tile j+1 interleaved with the softmax of tile j, masking of the
+    // diagonal and last tiles, and the row-max fix-up.  It leaves m and l in registers
+    // and this wave's O in LDS.
+    typedef __attribute__((address_space(3))) T lds_t;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_t*)smem);
+    uint32_t p_ka[KS], p_va[2][DB];
+#pragma unroll
+    for (int t = 0; t < KS; ++t) p_ka[t] = lds0 + 2 * kaddr[t];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) p_va[hf][db] = lds0 + 2 * vaddr[hf][db];
+    const uint32_t p_lbase = __builtin_amdgcn_readfirstlane(lds0 + ws * 64 * 16);
+    const uint32_t p_olds = lds0 + ws * 32768 + lane * 16;
+    int p_row[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) p_row[rb] = CAUSAL ? row[rb] : 0x3fffffff;
+    const int p_hh4 = hh * 4;
+    // copy resources of tile jbeg over the rows [jbeg*BN, min(nk, jend*BN)); each copy
+    // advances them by one tile, so rows past that range read as zeros
+    const int64_t rows_left = max((int64_t)min(nk, jend * BN) - (int64_t)jbeg * BN, (int64_t)0);
+    const uint64_t ka0 = (uint64_t)(uintptr_t)(kbase + (int64_t)jbeg * BN * p.k_ss);
+    const uint64_t va0 = (uint64_t)(uintptr_t)(vbase + (int64_t)jbeg * BN * p.v_ss);
+    const uint32_t pk_rs[4] = {(uint32_t)ka0, (uint32_t)(ka0 >> 32) & 0xffffu,
+                               (uint32_t)min(rows_left * p.k_ss * 2, (int64_t)0x7fffffff), 0x00020000u};
+    const uint32_t pv_rs[4] = {(uint32_t)va0, (uint32_t)(va0 >> 32) & 0xffffu,
+                               (uint32_t)min(rows_left * p.v_ss * 2, (int64_t)0x7fffffff), 0x00020000u};
+    const uint32_t p_ktb = (uint32_t)(BN * p.k_ss * 2), p_vtb = (uint32_t)(BN * p.v_ss * 2);
+    // tiles of this wave: [jbeg, jl]; causal waves stop at their diagonal tile, waves
+    // whose rows are all past the sequence have none
+    const int wrow0 = m0 + ws * RB * 32;
+    int jl = CAUSAL ? min(jend - 1, (wrow0 + RB * 32 - 1) / BN) : jend - 1;
+    if (wrow0 >= nq) jl = jbeg - 1;
+    const int p_jl = __builtin_amdgcn_readfirstlane(jl);
+    const int p_jbeg = jbeg, p_jend = jend, p_nk = nk;
+    const int p_wrow = CAUSAL ? wrow0 : 0x3fffffff;
+#ifdef FAL_PIPE_DEBUG_CYC
+    uint32_t p_dbg[4];
+#endif
+    if constexpr (std::is_same<T, half_t>::value)
+      asm volatile(FAL_PIPE_ASM_F16 : FAL_PIPE_OUTS : FAL_PIPE_INS : FAL_PIPE_CLOBBERS);
+    else
+      asm volatile(FAL_PIPE_ASM_BF16 : FAL_PIPE_OUTS : FAL_PIPE_INS : FAL_PIPE_CLOBBERS);
+    const char* ob = (const char*)smem + ws * 32768 + lane * 16;
+#ifdef FAL_PIPE_DEBUG_CYC
+    if (lane == 0 && m0 == 0 && hq == 0 && b == 0) {
+      // debug build: per-wave cycle sums (PV phase, wait + barrier, S phase, iterations)
+      for (int i = 0; i < 4; ++i) obase[ws * 4 + i] = (T)((float)p_dbg[i] / (i < 3 ? 1024.f : 1.f));
+      return;
+    }
+#endif
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(ob + ((rb * DB + db) * 4 + g4) * 1024);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) oacc[rb][db][g4 * 4 + e] = x[e];
+        }
+  } else {
   if (jbeg < jend) load_tile(jbeg, 0);
   // Tiles that need no mask for any row of the workgroup: straight-line, unrolled by
   // two so both LDS buffer offsets are constants (tile j uses buffer (j - jbeg) & 1).
@@ -423,12 +505,13 @@ fwd_kernel(FwdParams p) {
   }
   // Diagonal and tail tiles; waves whose rows all precede the tile only keep the
   // pipeline (barrier + prefetch) going.
-  const int wrow_hi = m0 + (w * RB + RB - 1) * 32 + 31;   // last query row of this wave
   for (; j < jend; ++j) {
     wait_vmcnt0();
     __syncthreads();
     if (j + 1 < jend) load_tile(j + 1, (j + 1 - jbeg) & 1);
     if (!CAUSAL || j * BN <= wrow_hi) tile_body(std::true_type{}, j, (j - jbeg) & 1);
+  }
+
   }
 
   if (p.kchunk) {
@@ -644,7 +727,7 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
 // Host-side launchers
 // ---------------------------------------------------------------------------
 #ifndef FAL_FWD_RB128
-#define FAL_FWD_RB128 1   // 32-row blocks per wave for head_dim 128
+#define FAL_FWD_RB128 2   // 32-row blocks per wave for head_dim 128 (2: the pipelined loop)
 #endif
 #ifndef FAL_FWD_NW128
 #define FAL_FWD_NW128 4   // waves per workgroup for head_dim 128
@@ -661,16 +744,21 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
 #ifndef FAL_FWD_RB64
 #define FAL_FWD_RB64 1
 #endif
-template <int D>
+#ifndef FAL_FWD_RB128_VARLEN
+#define FAL_FWD_RB128_VARLEN 1   // varlen keeps 128-row tiles (less waste on short sequences: +3% on C4)
+#endif
+// VARLEN: the configuration of packed-sequence calls (cu_seqlens set)
+template <int D, bool VARLEN = false>
 struct FwdCfg {
   static constexpr int NW = D == 128 ? FAL_FWD_NW128 : 4;
   static constexpr int BN = (D >= 256) ? 32 : D == 32 ? FAL_FWD_BN32 : D == 64 ? FAL_FWD_BN64 : FAL_FWD_BN;
-  static constexpr int RB = D == 128 ? FAL_FWD_RB128 : D == 32 ? FAL_FWD_RB32 : D == 64 ? FAL_FWD_RB64 : 1;
+  static constexpr int RB = D == 128 ? (VARLEN ? FAL_FWD_RB128_VARLEN : FAL_FWD_RB128)
+                            : D == 32 ? FAL_FWD_RB32 : D == 64 ? FAL_FWD_RB64 : 1;
 };
 
-template <class T, int D>
+template <class T, int D, bool VARLEN>
 static hipError_t launch_fwd_t(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
-  constexpr int NW = FwdCfg<D>::NW, BN = FwdCfg<D>::BN, RB = FwdCfg<D>::RB;
+  constexpr int NW = FwdCfg<D, VARLEN>::NW, BN = FwdCfg<D, VARLEN>::BN, RB = FwdCfg<D, VARLEN>::RB;
   if (causal)
     hipLaunchKernelGGL((fwd_kernel<T, D, NW, BN, true, RB>), grid, dim3(NW * 64), 0, st, p);
   else
@@ -679,11 +767,15 @@ static hipError_t launch_fwd_t(const FwdParams& p, int causal, dim3 grid, hipStr
 }
 template <int D>
 static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
-  return p.bf16 ? launch_fwd_t<bf16_t, D>(p, causal, grid, st) : launch_fwd_t<half_t, D>(p, causal, grid, st);
+  if (p.cu_q)
+    return p.bf16 ? launch_fwd_t<bf16_t, D, true>(p, causal, grid, st)
+                  : launch_fwd_t<half_t, D, true>(p, causal, grid, st);
+  return p.bf16 ? launch_fwd_t<bf16_t, D, false>(p, causal, grid, st)
+                : launch_fwd_t<half_t, D, false>(p, causal, grid, st);
 }
 
-template <int D>
-constexpr int fwd_bm() { return FwdCfg<D>::NW * 32 * FwdCfg<D>::RB; }
+template <int D, bool VARLEN = false>
+constexpr int fwd_bm() { return FwdCfg<D, VARLEN>::NW * 32 * FwdCfg<D, VARLEN>::RB; }
 
 template <int D>
 constexpr int fwd_bn() { return FwdCfg<D>::BN; }
@@ -773,6 +865,16 @@ int fwd_block_m(int d) {
     case 96: return fwd_bm<96>();
     case 128: return fwd_bm<128>();
     default: return fwd_bm<256>();
+  }
+}
+
+int fwd_block_m_varlen(int d) {
+  switch (d) {
+    case 32: return fwd_bm<32, true>();
+    case 64: return fwd_bm<64, true>();
+    case 96: return fwd_bm<96, true>();
+    case 128: return fwd_bm<128, true>();
+    default: return fwd_bm<256, true>();
   }
 }
 

@@ -107,6 +107,7 @@ struct DecodeParams {
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 int fwd_block_m(int d);
+int fwd_block_m_varlen(int d);   // query rows per workgroup of a packed-sequence call
 int fwd_block_n(int d);
 // Split-KV plan for a batched forward: sets kchunk / nsplit (kchunk 0 = no split) and
 // returns the workspace bytes the split needs (0 without a split).
