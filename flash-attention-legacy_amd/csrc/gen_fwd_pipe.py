@@ -66,9 +66,11 @@ SM, SM0 = 84, 86
 SK, SV = 88, 92
 SJ, SD, ST, ST2 = 96, 97, 98, 99
 NEG_INF = "0xff800000"
-# FAL_PIPE_ABL (measurement builds only, results are wrong): comma-separated subset of
+# Measurement builds only (FAL_PIPE_MEASURE=1; their results are wrong, so a stray
+# variable never reaches a normal build).  FAL_PIPE_ABL: comma-separated subset of
 # nodma, nowait, nobar, novalu, nolds
-ABL = set(x for x in os.environ.get("FAL_PIPE_ABL", "").split(",") if x)
+MEASURE = os.environ.get("FAL_PIPE_MEASURE") == "1"
+ABL = set(x for x in os.environ.get("FAL_PIPE_ABL", "").split(",") if x) if MEASURE else set()
 
 # ---- operands: (name, constraint, C++ expression) ----
 OUTS = [("m0", "+v", "m_run[0]"), ("m1", "+v", "m_run[1]"), ("l0", "+v", "l_run[0]"), ("l1", "+v", "l_run[1]")]
@@ -93,7 +95,10 @@ for i in range(4):
 INS += [("c", "s", "c"), ("jbeg", "s", "p_jbeg"), ("jend", "s", "p_jend"), ("jl", "s", "p_jl"),
         ("wrow", "s", "p_wrow"), ("nk", "s", "p_nk"), ("ktb", "s", "p_ktb"), ("vtb", "s", "p_vtb"),
         ("lbase", "s", "p_lbase")]
-DBG_CYC = os.environ.get("FAL_PIPE_DEBUG") == "CYC"
+# FAL_PIPE_DEBUG=CYC: per-wave cycle sums of the iteration phases; =S: raw scores of the
+# first tile instead of O
+DEBUG = os.environ.get("FAL_PIPE_DEBUG") if MEASURE else None
+DBG_CYC = DEBUG == "CYC"
 if DBG_CYC:
     OUTS += [(f"dbg{i}", "=s", f"p_dbg[{i}]") for i in range(4)]
 IDX = {name: i for i, (name, _, _) in enumerate(OUTS + INS)}
@@ -480,7 +485,7 @@ class Emitter:
         e(f"s_cbranch_scc1 {L('disp', shared=True)}")
         self.es(self.slot(f"s{ST}", 0))
         self.s_simple(0)
-        if os.environ.get("FAL_PIPE_DEBUG") == "S":
+        if DEBUG == "S":
             # debug: raw S^T of the first tile to the O hand-off area, l = 1/2 per lane
             e("s_nop 15")
             for g in range(16):
@@ -587,7 +592,7 @@ class Emitter:
         if DBG_CYC:
             for i, r in enumerate((78, 79, 82, 83)):
                 e(f"s_mov_b32 {op(f'dbg{i}')}, s{r}")
-        if os.environ.get("FAL_PIPE_DEBUG") == "S":
+        if DEBUG == "S":
             e(f"{L('dbgout', shared=True)}:")
         return self.lines
 
