@@ -43,6 +43,9 @@ namespace fal {
 #ifndef FAL_FWD_KDEPTH
 #define FAL_FWD_KDEPTH 2
 #endif
+#ifndef FAL_FWD_SUM_F32
+#define FAL_FWD_SUM_F32 1   // row sums: 1 = fp32 adds of exp2 values, 0 = v_dot2c of the packed P
+#endif
 #ifndef FAL_FWD_PIPE
 #define FAL_FWD_PIPE 1   // head_dim 128 at two row blocks per wave: software-pipelined tile loop
 #endif
@@ -353,10 +356,20 @@ fwd_kernel(FwdParams p) {
 #pragma unroll
           for (int t2 = 0; t2 < 2; ++t2) {
             V8 h;
+#if FAL_FWD_SUM_F32
+            // fp32 adds of the exponentials (v_dot2c sums of the packed P stall the MFMAs)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float pe = fast_exp2(sacc[rb][kb][t2 * 8 + e]);
+              h[e] = (T)pe;
+              lt[rb] += pe;
+            }
+#else
 #pragma unroll
             for (int e = 0; e < 8; ++e) h[e] = (T)fast_exp2(sacc[rb][kb][t2 * 8 + e]);
-            pb[rb][kb][t2] = h;
             lt[rb] = sum8(h, lt[rb]);
+#endif
+            pb[rb][kb][t2] = h;
           }
       }
     };
