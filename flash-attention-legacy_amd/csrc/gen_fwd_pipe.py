@@ -50,13 +50,14 @@ import sys
 NBUF = 4            # LDS ring slots
 VOFF = 16384        # V offset inside a slot (bytes)
 KDIST = int(os.environ.get("FAL_PIPE_KDIST", "2"))   # K read-ahead (k-steps of 2 fragments)
-VDIST = 3           # V^T read-ahead (fragment pairs)
+VRING = int(os.environ.get("FAL_PIPE_VRING", "4"))   # V^T fragment ring (pairs of transposed reads)
+VDIST = int(os.environ.get("FAL_PIPE_VDIST", "3"))   # V^T read-ahead (fragment pairs), < VRING
 DMA_AUX = os.environ.get("FAL_PIPE_DMA_AUX", "")       # cache-policy bits of the tile copies
 GSTRIDE = int(os.environ.get("FAL_PIPE_GSTRIDE", "1"))   # MFMAs between two copy instructions
 
 SA = (128, 192)
-KF = 208            # AGPR
-VF = 240            # AGPR
+VF = 256 - 4 * VRING   # AGPR: V^T ring at the top, K ring below it
+KF = VF - 32
 KC = 112
 VC = 120
 LT = (104, 105)
@@ -222,14 +223,14 @@ class Emitter:
         reads, mf = [], []
         for ks in range(4):
             for db in range(4):
-                p = (ks * 4 + db) % 4
+                p = (ks * 4 + db) % VRING
                 for hf in range(2):
                     reads.append(f"ds_read_b64_tr_b16 {ar(VF + 4 * p + 2 * hf, 2)}, {v(VC + hf * 4 + db)} "
                                  f"offset:{VOFF + ks * 4096}")
         for ks in range(4):
             kb, t2 = ks // 2, ks % 2
             for db in range(4):
-                p = (ks * 4 + db) % 4
+                p = (ks * 4 + db) % VRING
                 for rb in range(2):
                     o = ar((rb * 4 + db) * 16, 16)
                     pb = vr(SA[par] + rb * 32 + kb * 16 + 4 * t2, 4)
@@ -608,7 +609,7 @@ def render():
     outs = ", ".join(f'"{c}"({x})' for _, c, x in OUTS)
     ins = ", ".join(f'"{c}"({x})' for _, c, x in INS)
     clob = ", ".join([f'"v{i}"' for i in range(104, 256)] + [f'"a{i}"' for i in range(0, 128)] +
-                     [f'"a{i}"' for i in range(208, 256)] + [f'"s{i}"' for i in range(76 if DBG_CYC else 84, 100)] +
+                     [f'"a{i}"' for i in range(KF, 256)] + [f'"s{i}"' for i in range(76 if DBG_CYC else 84, 100)] +
                      ['"vcc"', '"scc"', '"memory"'])
     out.append(f"#define FAL_PIPE_OUTS {outs}")
     out.append(f"#define FAL_PIPE_INS {ins}")
