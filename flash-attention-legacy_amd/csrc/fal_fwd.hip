@@ -469,6 +469,10 @@ fwd_kernel(FwdParams p) {
     const uint32_t pv_rs[4] = {(uint32_t)va0, (uint32_t)(va0 >> 32) & 0xffffu,
                                (uint32_t)min(rows_left * p.v_ss * 2, (int64_t)0x7fffffff), 0x00020000u};
     const uint32_t p_ktb = (uint32_t)(BN * p.k_ss * 2), p_vtb = (uint32_t)(BN * p.v_ss * 2);
+    // per-tile record counts: the tile's rows inside [jbeg*BN, min(nk, jend*BN)) times the
+    // row stride (a single count over the whole range could exceed 2^31 bytes)
+    const uint32_t p_krb = (uint32_t)(p.k_ss * 2), p_vrb = (uint32_t)(p.v_ss * 2);
+    const int p_rows = (int)rows_left;
     // tiles of this wave: [jbeg, jl]; causal waves stop at their diagonal tile, waves
     // whose rows are all past the sequence have none
     const int wrow0 = m0 + ws * RB * 32;

@@ -37,7 +37,8 @@ Register plan (per lane; one wave per SIMD: 256 VGPRs and 256 AGPRs):
                           registers of each 16-register block
   v[112:119], v[120:127]  K fragment and V^T LDS addresses of the current tile
   v104/v105 per-lane P sums, v106/v107 -m, v108..v111 temporaries
-  s[84:85] compare mask, s86 caller's m0, s[88:91]/s[92:95] K/V copy resources,
+  s[84:85] compare mask, s86 caller's m0, s87 rows left from the next tile to copy,
+  s[88:91]/s[92:95] K/V copy resources,
   s96 tile j, s97 next tile to copy, s98/s99 temporaries
   v0..v103, a128..a207 and s0..s83 are left to the compiler (Q arrives in AGPRs).
 
@@ -63,7 +64,7 @@ VC = 120
 LT = (104, 105)
 NM = (106, 107)
 T0, T1, T2, T3 = 108, 109, 110, 111
-SM, SM0 = 84, 86
+SM, SM0, SR = 84, 86, 87
 SK, SV = 88, 92
 SJ, SD, ST, ST2 = 96, 97, 98, 99
 NEG_INF = "0xff800000"
@@ -95,6 +96,7 @@ for i in range(4):
     INS.append((f"vr{i}", "s", f"pv_rs[{i}]"))
 INS += [("c", "s", "c"), ("jbeg", "s", "p_jbeg"), ("jend", "s", "p_jend"), ("jl", "s", "p_jl"),
         ("wrow", "s", "p_wrow"), ("nk", "s", "p_nk"), ("ktb", "s", "p_ktb"), ("vtb", "s", "p_vtb"),
+        ("krb", "s", "p_krb"), ("vrb", "s", "p_vrb"), ("rows", "s", "p_rows"),
         ("lbase", "s", "p_lbase")]
 # FAL_PIPE_DEBUG=CYC: per-wave cycle sums of the iteration phases; =S: raw scores of the
 # first tile instead of O
@@ -180,8 +182,12 @@ class Emitter:
     def dma_groups(self):
         """Copy of tile s97 into its slot (8 buffer->LDS loads), then the copy resources
         advance one tile (rows past the copy range read as zeros)."""
+        # record counts of this tile: its rows inside the copy range (0..64) times the
+        # row stride, so rows past the range read as zeros
         groups = [[f"s_and_b32 s{ST}, s{SD}, {NBUF - 1}", f"s_lshl_b32 s{ST}, s{ST}, 15",
-                   f"s_add_u32 s{ST}, s{ST}, {op('lbase')}"]]
+                   f"s_add_u32 s{ST}, s{ST}, {op('lbase')}",
+                   f"s_max_i32 s{SK + 2}, s{SR}, 0", f"s_min_i32 s{SK + 2}, s{SK + 2}, 64",
+                   f"s_mul_i32 s{SV + 2}, s{SK + 2}, {op('vrb')}", f"s_mul_i32 s{SK + 2}, s{SK + 2}, {op('krb')}"]]
         for part, rs, vo in (("k", SK, "kvo"), ("v", SV, "vvo")):
             for i in range(4):
                 off = i * 4096 + (VOFF if part == "v" else 0)
@@ -192,9 +198,8 @@ class Emitter:
             return groups
         groups.append([
             f"s_add_u32 s{SK}, s{SK}, {op('ktb')}", f"s_addc_u32 s{SK + 1}, s{SK + 1}, 0",
-            f"s_sub_u32 s{SK + 2}, s{SK + 2}, {op('ktb')}", f"s_cselect_b32 s{SK + 2}, 0, s{SK + 2}",
             f"s_add_u32 s{SV}, s{SV}, {op('vtb')}", f"s_addc_u32 s{SV + 1}, s{SV + 1}, 0",
-            f"s_sub_u32 s{SV + 2}, s{SV + 2}, {op('vtb')}", f"s_cselect_b32 s{SV + 2}, 0, s{SV + 2}",
+            f"s_sub_i32 s{SR}, s{SR}, 64",
             f"s_add_u32 s{SD}, s{SD}, 1"])
         return groups
 
@@ -467,10 +472,10 @@ class Emitter:
         for i in range(4):
             e(f"s_mov_b32 s{SK + i}, {op(f'kr{i}')}")
             e(f"s_mov_b32 s{SV + i}, {op(f'vr{i}')}")
-        if "dmazero" in ABL:
-            e(f"s_mov_b32 s{SK + 2}, 0")
-            e(f"s_mov_b32 s{SV + 2}, 0")
         e(f"s_mov_b32 s{SJ}, {op('jbeg')}")
+        e(f"s_mov_b32 s{SR}, {op('rows')}")
+        if "dmazero" in ABL:
+            e(f"s_mov_b32 s{SR}, 0")
         e(f"s_mov_b32 s{SD}, {op('jbeg')}")
         for a in range(128):
             e(f"v_accvgpr_write_b32 a{a}, 0")

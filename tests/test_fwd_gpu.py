@@ -262,3 +262,26 @@ def test_split_kv_small_grid(d, causal, nq, nk):
     fin = torch.isfinite(ref_l)
     assert torch.equal(torch.isfinite(lse.cpu()), fin)
     assert max_abs(lse.cpu()[fin], ref_l[fin]) <= 1e-3
+
+
+def test_head_slice_beyond_2gib():
+    """K/V stored with the heads interleaved in each row ([B, N, H, d] viewed as
+    [B, H, N, d]) and N = 2^20 + 4096 keys: one head's rows span 2.15 GB, more than a
+    buffer resource's 2^31-byte record count, so the copies must bound each tile
+    separately.  Sampled rows of the first and last head against exact float64 rows."""
+    Hkv, d, nq = 8, 128, 8192     # 256 workgroups: no split of the key range
+    nk = (1 << 20) + 4096
+    assert ext()._lib.fal_fwd_workspace_size(1, Hkv, nq, nk, d, 0) == 0
+    g = torch.Generator(device="cuda").manual_seed(70)
+    k = torch.randn((1, nk, Hkv, d), generator=g, device="cuda", dtype=torch.float16)
+    v = torch.randn((1, nk, Hkv, d), generator=g, device="cuda", dtype=torch.float16)
+    q = randn((1, Hkv, nq, d), seed=71)
+    kv, vv = k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3)
+    assert kv.stride(2) * 2 * nk > 2 ** 31
+    scale = 1.0 / math.sqrt(d)
+    o, lse = ext().forward(q, kv, vv, scale, False)
+    rows = [0, 4095, nq - 1]
+    for h in (0, Hkv - 1):
+        ref_o, ref_l = exact_rows(q[0, h], kv[0, h], vv[0, h], rows, scale, False)
+        assert max_abs(o[0, h, rows], torch.from_numpy(ref_o)) <= FWD_ATOL, h
+        assert float(np.abs(lse[0, h, rows].cpu().numpy() - ref_l).max()) <= 1e-3, h
