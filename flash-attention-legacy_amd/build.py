@@ -60,11 +60,13 @@ def _compile(src: str, verbose: bool, objdir: str = OBJ, defines=()) -> str:
 def build(jobs: int | None = None, verbose: bool = False, out: str = OUT, defines=()) -> str:
     """Compile and link; returns the path of the shared library.  `defines` are extra
     NAME=VALUE macros (kernel tunables); `out` is the library path to write."""
-    # the pipelined forward loop is generated text (csrc/gen_fwd_pipe.py)
+    # the pipelined forward and dK/dV loops are generated text (csrc/gen_*_pipe.py)
     sys.path.insert(0, CSRC)
     try:
+        import gen_bwd_pipe
         import gen_fwd_pipe
         gen_fwd_pipe.main()
+        gen_bwd_pipe.main()
     finally:
         sys.path.remove(CSRC)
     objdir = OBJ if not defines else os.path.join(OBJ, "_".join(defines).replace("=", "-"))

@@ -290,9 +290,17 @@ static size_t bwd_acc_bytes(size_t rows, int64_t head_dim) {
   return bwd_split_dq(head_dim_ok(head_dim) ? (int)head_dim : 0) ? 0 : align256(rows * head_dim * sizeof(float));
 }
 
+// Batched head_dim 128 also holds the lsd array: per (batch, query head, 64-row tile)
+// 64 values of -L*log2(e)/c and 64 of -D.
+static size_t bwd_lsd_bytes(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t head_dim) {
+  if (!head_dim_ok(head_dim) || !bwd_pipe((int)head_dim)) return 0;
+  return align256((size_t)batch * heads_q * ((seqlen_q + 63) / 64) * 128 * sizeof(float));
+}
+
 size_t fal_bwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, int64_t head_dim) {
   const size_t rows = (size_t)batch * heads_q * seqlen_q;
-  return bwd_acc_bytes(rows, head_dim) + align256(rows * sizeof(float));
+  return bwd_acc_bytes(rows, head_dim) + align256(rows * sizeof(float)) +
+         bwd_lsd_bytes(batch, heads_q, seqlen_q, head_dim);
 }
 
 static int fill_bwd_common(BwdParams& p, const void* dout, const void* q, const void* k, const void* v,
@@ -373,6 +381,8 @@ static int fal_bwd_impl(const void* dout, const void* q, const void* k, const vo
   const size_t acc = bwd_acc_bytes(rows, head_dim);
   p.dq_acc = acc ? static_cast<float*>(workspace) : nullptr;
   p.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc);
+  if (bwd_lsd_bytes(batch, heads_q, seqlen_q, head_dim))
+    p.lsd = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc + align256(rows * sizeof(float)));
   p.dqa_sb = heads_q * seqlen_q * head_dim; p.dqa_sh = seqlen_q * head_dim; p.dqa_ss = head_dim;
   p.l_sb = heads_q * seqlen_q; p.l_sh = seqlen_q; p.l_ss = 1;
   p.B = (int)batch; p.Hq = (int)heads_q; p.Hkv = (int)heads_kv;

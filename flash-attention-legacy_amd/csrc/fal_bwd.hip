@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "fal_kernels.h"
+#include "fal_bwd_pipe.inc"
 
 namespace fal {
 
@@ -810,6 +811,160 @@ bwd2_kernel(BwdParams p) {
 
 
 // --------------------------------------------------------------------------
+// dK/dV kernel for head_dim 128, batched (bwd_kv_pipe_kernel): one wave per SIMD and a
+// software-pipelined query-tile loop written as one inline-asm block (fal_bwd_pipe.inc,
+// generated by gen_bwd_pipe.py).  A workgroup owns 128 keys of one KV head, each wave
+// 32 keys whose K and V fragments stay in registers; the items (query head of the
+// group, 64-row query tile) stream through a 4-slot LDS ring of Q/dO tiles copied two
+// items ahead.  Per item the S and dP accumulators start at -L*log2(e)/c and -D, read
+// from the tile-major array `lsd` that bwd_dq_kernel writes, so P = exp2(c*S) and
+// dS = P*dP.  The products of item i-1 (dV^T += dO^T P, dK^T += Q^T dS), the
+// exponentials of item i and the products of item i+1 (S = Q K^T, dP = dO V^T)
+// overlap inside the wave; no cross-wave sum is needed.  Same math as bwd2_kernel.
+// --------------------------------------------------------------------------
+#ifndef FAL_BWD_PIPE
+#define FAL_BWD_PIPE 1
+#endif
+constexpr int kPipeBN = 128;    // keys per workgroup
+constexpr int kPipeBM = 64;     // query rows per item
+
+template <class T, bool CAUSAL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+bwd_kv_pipe_kernel(BwdParams p) {
+  using V8 = vec8<T>;
+  using V4 = vec4<T>;
+  using TL = SwizzledTile<128>;
+  constexpr int CPR = TL::CPR;
+  // 4 slots of (Q tile, dO tile) and 4 slots of (64 Ls, 64 Dn) values
+  __shared__ __attribute__((aligned(1024))) char smem[4 * 32768 + 4 * 512];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int ws = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+
+  // work item: one or two 128-key tiles of one (batch, KV head); causal tiles are
+  // paired (kt, n-1-kt) so every workgroup has the same number of items
+  const int nkt = cdiv(p.Nk, kPipeBN);
+  const int total = gridDim.x;
+  int id = blockIdx.x;
+  if ((total & 7) == 0) id = (id & 7) * (total >> 3) + (id >> 3);
+  const int nk_items = CAUSAL ? (nkt + 1) / 2 : nkt;
+  const int kit = id % nk_items;
+  const int bh = id / nk_items;
+  const int b = bh / p.Hkv, hkv = bh % p.Hkv;
+  const int kt_b = (CAUSAL && nkt - 1 - kit != kit) ? nkt - 1 - kit : -1;
+  const int G = p.Hq / p.Hkv;
+  const int nq = p.Nq, nk = p.Nk;
+  const int nqt = cdiv(nq, kPipeBM);
+
+  typedef __attribute__((address_space(3))) char lds_t;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_t*)smem);
+  // per-lane LDS addresses: fragment (row l32, chunk 2t+hh) and transposed reads
+  // (rows hf*8 + hh*4 + i/4 of a 16-row step, 32-column block db) of a slot's tiles
+  uint32_t p_qa[8], p_ta[2][4];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) p_qa[t] = lds0 + 2 * TL::offset(l32, 2 * t + hh);
+  {
+    const int i = lane & 15;
+    const int rl = hh * 4 + (i >> 2);
+    const int cl = 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) p_ta[hf][db] = lds0 + 2 * (TL::offset(hf * 8 + rl, db * 4 + cl) + 4 * (lane & 1));
+  }
+  const uint32_t p_la = lds0 + 131072 + 16 * hh;
+  // copy offsets: load i of wave ws fills chunks [(4i + ws)*64, +64) of a tile
+  int p_qo[4], p_do[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pch = (i * 4 + ws) * 64 + lane;
+    const int r = pch / CPR;
+    const int cc = TL::logical_chunk(r, pch % CPR);
+    p_qo[i] = (int)(r * p.q_ss + cc * 8) * 2;
+    p_do[i] = (int)(r * p.do_ss + cc * 8) * 2;
+  }
+  const int p_lo4 = lane * 4, p_lo4b = 256 + lane * 4;
+  const int p_lk = l32 - 4 * hh;
+  const uint32_t p_olds = lds0 + ws * 16384 + lane * 8;
+  const uint32_t p_lbase = __builtin_amdgcn_readfirstlane(lds0 + ws * 1024);
+  const uint32_t p_ldbase = __builtin_amdgcn_readfirstlane(lds0 + 131072);
+  const float p_c = p.scale_log2;
+  const float p_negc = p.scale_log2 > 0.f ? -INFINITY : INFINITY;   // c * negc = -inf
+  const float p_scale = p.scale;
+  const uint32_t p_qrb = (uint32_t)(p.q_ss * 2), p_drb = (uint32_t)(p.do_ss * 2);
+  const int p_nq = nq, p_nqt = nqt;
+  const int64_t qstep = (int64_t)kPipeBM * p.q_ss * 2, dstep = (int64_t)kPipeBM * p.do_ss * 2;
+
+  for (int tile_i = 0; tile_i < 2; ++tile_i) {
+    const int kt = tile_i == 0 ? kit : kt_b;
+    if (kt < 0) break;
+    const int n0 = kt * kPipeBN;
+    const int kw0 = n0 + ws * 32;
+    const int key = kw0 + l32;
+    const int qt0 = CAUSAL ? n0 / kPipeBM : 0;
+    const int ntq = max(nqt - qt0, 0);
+    const int nitems = G * ntq;
+    const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
+    const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
+    V8 kreg[8], vreg[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      kreg[t] = key < nk ? ld8(kbase + (int64_t)key * p.k_ss + t * 16 + hh * 8) : zero8<T>();
+      vreg[t] = key < nk ? ld8(vbase + (int64_t)key * p.v_ss + t * 16 + hh * 8) : zero8<T>();
+    }
+    __syncthreads();   // the previous tile's epilogue readers are done with the LDS
+    const char* ob = smem + ws * 16384 + lane * 8;
+    if (nitems > 0) {
+      const int hq0 = hkv * G;
+      const uint64_t qb = (uint64_t)(uintptr_t)((const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq0 * p.q_sh +
+                                                (int64_t)qt0 * kPipeBM * p.q_ss);
+      const uint64_t dob = (uint64_t)(uintptr_t)((const T*)p.dout + (int64_t)b * p.do_sb +
+                                                 (int64_t)hq0 * p.do_sh + (int64_t)qt0 * kPipeBM * p.do_ss);
+      const uint64_t lb = (uint64_t)(uintptr_t)(p.lsd + (((int64_t)b * p.Hq + hq0) * nqt + qt0) * 2 * kPipeBM);
+      const int64_t qwrap = p.q_sh * 2 - (int64_t)(ntq - 1) * qstep;
+      const int64_t dwrap = p.do_sh * 2 - (int64_t)(ntq - 1) * dstep;
+      const uint32_t p_qb_lo = (uint32_t)qb, p_qb_hi = (uint32_t)(qb >> 32) & 0xffffu;
+      const uint32_t p_db_lo = (uint32_t)dob, p_db_hi = (uint32_t)(dob >> 32) & 0xffffu;
+      const uint32_t p_lb_lo = (uint32_t)lb, p_lb_hi = (uint32_t)(lb >> 32) & 0xffffu;
+      const uint32_t p_qs_lo = (uint32_t)qstep, p_qs_hi = (uint32_t)((uint64_t)qstep >> 32);
+      const uint32_t p_qw_lo = (uint32_t)qwrap, p_qw_hi = (uint32_t)((uint64_t)qwrap >> 32);
+      const uint32_t p_ds_lo = (uint32_t)dstep, p_ds_hi = (uint32_t)((uint64_t)dstep >> 32);
+      const uint32_t p_dw_lo = (uint32_t)dwrap, p_dw_hi = (uint32_t)((uint64_t)dwrap >> 32);
+      const uint32_t p_ldw = (uint32_t)(1 + qt0) * 2 * kPipeBM * 4;   // last tile of a head -> first of the next
+      const int p_qt0 = qt0, p_nitems = nitems;
+      const int p_kw0 = CAUSAL ? kw0 : -(1 << 30);
+      if constexpr (std::is_same<T, half_t>::value)
+        asm volatile(FAL_BWDP_ASM_F16 : FAL_BWDP_OUTS : FAL_BWDP_INS : FAL_BWDP_CLOBBERS);
+      else
+        asm volatile(FAL_BWDP_ASM_BF16 : FAL_BWDP_OUTS : FAL_BWDP_INS : FAL_BWDP_CLOBBERS);
+    }
+    // dV then dK*scale of this wave's keys: piece (db, g4) holds columns
+    // db*32 + g4*8 + hh*4 .. +3 of key `key`
+    if (key < nk) {
+      T* dvrow = (T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + (int64_t)key * p.dv_ss;
+      T* dkrow = (T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + (int64_t)key * p.dk_ss;
+#pragma unroll
+      for (int pc = 0; pc < 16; ++pc) {
+        const int col = (pc >> 2) * 32 + (pc & 3) * 8 + hh * 4;
+        V4 hv, hk;
+        if (nitems > 0) {
+          hv = *reinterpret_cast<const V4*>(ob + pc * 512);
+          hk = *reinterpret_cast<const V4*>(ob + 8192 + pc * 512);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hv[e] = hk[e] = (T)0.f;
+        }
+        *reinterpret_cast<V4*>(dvrow + col) = hv;
+        *reinterpret_cast<V4*>(dkrow + col) = hk;
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
 // Query-outer dQ kernel for head_dim 32, 64, 96 and 128 (the KV-outer kernel above then
 // produces only dK/dV).  Same structure as the forward kernel: a workgroup owns
 // 32*NW query rows of one query head, each wave 32 rows whose Q and dO slices stay
@@ -927,6 +1082,18 @@ bwd_dq_kernel(BwdParams p) {
   const float drow = pair_sum(dpart);
   if (hh == 0 && row < nq) p.delta[lrow + (int64_t)row * p.l_ss] = drow;
   const float c = p.scale_log2;
+  if (p.lsd && hh == 0) {
+    // tile-major copy for bwd_kv_pipe_kernel, 64 rows per tile: -L*log2(e)/c, then -D.
+    // Rows past the end (up to the tile boundary) and rows without keys get the value
+    // whose exponent c * x is -inf, and -D = 0.
+    const int nt64 = cdiv(nq, kPipeBM);
+    if (row < nt64 * kPipeBM) {
+      float* t = p.lsd + (((int64_t)b * p.Hq + hq) * nt64 + row / kPipeBM) * 2 * kPipeBM + row % kPipeBM;
+      const bool live = row < nq && lrow2 != INFINITY;
+      t[0] = live ? -lrow2 / c : (c > 0.f ? -INFINITY : INFINITY);
+      t[kPipeBM] = row < nq ? -drow : 0.f;
+    }
+  }
 
   const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
   const int ntiles = cdiv(kend, BN);
@@ -1096,8 +1263,21 @@ int bwd_block_n(int d) {
   return split_d(d) ? FAL_BWD2_NW * 16 : kBwdNW * 32;
 }
 
+bool bwd_pipe(int d) { return FAL_BWD_PIPE && d == 128; }
+
 template <class T, int D>
 static hipError_t launch_bwd_t(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (!p.cu_q && p.lsd) {
+      const int nkt = cdiv(p.Nk, kPipeBN);
+      grid.x = (unsigned)((causal ? (nkt + 1) / 2 : nkt) * p.B * p.Hkv);
+      if (causal)
+        hipLaunchKernelGGL((bwd_kv_pipe_kernel<T, true>), grid, dim3(256), 0, st, p);
+      else
+        hipLaunchKernelGGL((bwd_kv_pipe_kernel<T, false>), grid, dim3(256), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   if constexpr (split_d(D)) {
     constexpr bool kFused = fused_d(D);
     // batched causal: one workgroup per pair of key tiles

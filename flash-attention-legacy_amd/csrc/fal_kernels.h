@@ -79,6 +79,7 @@ struct BwdParams {
   int total_q;        // varlen: rows of the packed Q (row-wise kernels)
   int total_k;        // varlen: rows of the packed K/V
   int bf16;           // element type of every fp16/bf16 tensor: 0 fp16, 1 bf16
+  float* lsd;         // batched head_dim 128: per 64-row tile, -L*log2(e)/c then -D (null: unused)
 };
 
 // KV-cache decode (one query token per sequence).
@@ -144,6 +145,8 @@ hipError_t launch_bwd_post(const BwdParams& p, int d, hipStream_t st);
 // head dims whose dQ comes from the query-outer kernel (no fp32 accumulator)
 bool bwd_split_dq(int d);
 int bwd_dq_block_m(int d);
+// batched head_dim d uses bwd_kv_pipe_kernel (workspace holds the lsd array)
+bool bwd_pipe(int d);
 hipError_t launch_bwd_dq(const BwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 
 int decode_chunk(int d, int B, int Hkv, int max_seqlen);

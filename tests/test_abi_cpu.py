@@ -113,11 +113,14 @@ def test_forward_split_workspace(lib):
 
 
 def test_workspace_sizes_and_checks(lib):
-    # d 32/64/96/128: delta only (the query-outer dQ kernel needs no fp32 accumulator);
-    # d 256: delta + the fp32 dQ accumulator of the atomic kernel
+    # d 32/64/96: delta only (the query-outer dQ kernel needs no fp32 accumulator);
+    # d 128: delta + the tile-major (-L*log2e/c, -D) array of the pipelined dK/dV kernel,
+    # 64-row tiles (rounded up); d 256: delta + the fp32 dQ accumulator of the atomic kernel
     rows = 2 * 16 * 2048
-    for d in (32, 64, 96, 128):
+    for d in (32, 64, 96):
         assert rows * 4 <= lib.fal_bwd_workspace_size(2, 16, 2048, d) < rows * 4 + 4096
+    assert rows * 12 <= lib.fal_bwd_workspace_size(2, 16, 2048, 128) < rows * 12 + 4096
+    assert lib.fal_bwd_workspace_size(1, 1, 65, 128) >= 65 * 4 + 2 * 128 * 4
     assert lib.fal_bwd_workspace_size(2, 16, 2048, 256) >= rows * 257 * 4
     # small problems (<= 64 sequences, <= 16384 query tokens) derive their work items in
     # the kernel: no workspace; larger ones get a (sequence, tile) list
