@@ -65,6 +65,11 @@ SM = 88
 ST0, ST1, ST2, ST3, ST4 = 90, 91, 92, 93, 95
 SF = 94
 RSRC_W3 = "0x00020000"
+# Measurement builds only (FAL_BWDP_MEASURE=1; their results are wrong, so a stray
+# variable never reaches a normal build).  FAL_BWDP_ABL: comma-separated subset of
+# nodma, nobar, novalu, nolds, nob (no dV/dK products), noa (no S/dP products)
+MEASURE = os.environ.get("FAL_BWDP_MEASURE") == "1"
+ABL = set(x for x in os.environ.get("FAL_BWDP_ABL", "").split(",") if x) if MEASURE else set()
 
 # ---- operands: (name, constraint, C++ expression) ----
 OUTS = []
@@ -113,6 +118,7 @@ class Emitter:
         self.mf = "v_mfma_f32_32x32x16_bf16" if bf16 else "v_mfma_f32_32x32x16_f16"
         self.cvt = "v_cvt_pk_bf16_f32" if bf16 else "v_cvt_pk_f16_f32"
         self.nlabel = 0
+        self.skip_mf = False
 
     def e(self, s):
         self.lines.append(s)
@@ -127,6 +133,11 @@ class Emitter:
 
     # -- instruction streams ---------------------------------------------------
     def grad_ops(self, par, rb):
+        if "novalu" in ABL:
+            return []
+        return self._grad_ops(par, rb)
+
+    def _grad_ops(self, par, rb):
         """P = exp2(c*S) and dS = P*dP for row block rb of the item in SET[par], then
         both packed in place (pair k of elements 2k, 2k+1 into register k).  Streamed so
         the quarter-rate exponentials spread between the MFMAs: the multiply by c runs
@@ -210,10 +221,13 @@ class Emitter:
         for k, (ins, need) in enumerate(mf):
             target = min(len(reads) - 1, need + dist)
             while issued <= target:
-                self.e(reads[issued])
+                if "nolds" not in ABL:
+                    self.e(reads[issued])
                 issued += 1
-            self.e(f"s_waitcnt lgkmcnt({min(issued - need - 1, 15)})")
-            self.e(ins)
+            if "nolds" not in ABL:
+                self.e(f"s_waitcnt lgkmcnt({min(issued - need - 1, 15)})")
+            if not self.skip_mf:
+                self.e(ins)
             if groups:
                 self.es(groups.pop(0))
             goal = total * (k + 1) / len(mf)
@@ -254,12 +268,12 @@ class Emitter:
             f"s_lshl_b32 s{ST3}, s{ST3}, 9", f"s_add_u32 s{ST3}, s{ST3}, {op('ldbase')}"]]
         for part, rs, vo, base in (("q", SQ, "qo", 0), ("d", SD, "do", DOFF)):
             for i in range(4):
-                g.append([f"s_add_u32 m0, s{ST2}, {base + i * 4096}", "s_nop 0",
-                          f"buffer_load_dwordx4 {op(f'{vo}{i}')}, s[{rs}:{rs + 3}], 0 offen lds"])
-        g.append([f"s_mov_b32 m0, s{ST3}", "s_nop 0",
-                  f"buffer_load_dword {op('lo4')}, s[{SL}:{SL + 3}], 0 offen lds"])
-        g.append([f"s_add_u32 m0, s{ST3}, 256", "s_nop 0",
-                  f"buffer_load_dword {op('lo4b')}, s[{SL}:{SL + 3}], 0 offen lds"])
+                g.append([f"s_add_u32 m0, s{ST2}, {base + i * 4096}", "s_nop 0"] + ([] if "nodma" in ABL else
+                          [f"buffer_load_dwordx4 {op(f'{vo}{i}')}, s[{rs}:{rs + 3}], 0 offen lds"]))
+        g.append([f"s_mov_b32 m0, s{ST3}", "s_nop 0"] + ([] if "nodma" in ABL else
+                 [f"buffer_load_dword {op('lo4')}, s[{SL}:{SL + 3}], 0 offen lds"]))
+        g.append([f"s_add_u32 m0, s{ST3}, 256", "s_nop 0"] + ([] if "nodma" in ABL else
+                 [f"buffer_load_dword {op('lo4b')}, s[{SL}:{SL + 3}], 0 offen lds"]))
         g.append([
             f"s_add_u32 s{SQF}, s{SQF}, 1", f"s_cmp_eq_u32 s{SQF}, {op('nqt')}",
             f"s_cselect_b32 s{ST0}, {op('qw_lo')}, {op('qs_lo')}", f"s_cselect_b32 s{ST1}, {op('qw_hi')}, {op('qs_hi')}",
@@ -311,16 +325,21 @@ class Emitter:
         v0 = self.grad_ops(par, 0) if has_v else []
         if has_b:
             reads, mf = self.b_prod(par ^ 1)
+            self.skip_mf = "nob" in ABL
             self.interleave(reads, mf, BDIST, v0, self.dma_groups())
+            self.skip_mf = False
         else:
             self.dma()
             self.es(v0)
         e("s_waitcnt vmcnt(10)")
-        e("s_barrier")
+        if "nobar" not in ABL:
+            e("s_barrier")
         v1 = self.grad_ops(par, 1) if has_v else []
         if has_a:
             reads, mf = self.a_prod(par ^ 1)
+            self.skip_mf = "noa" in ABL
             self.interleave(reads, mf, ADIST, v1)
+            self.skip_mf = False
         else:
             self.es(v1)
         e(f"s_branch {lbl_next}")
