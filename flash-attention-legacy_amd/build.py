@@ -64,9 +64,11 @@ def build(jobs: int | None = None, verbose: bool = False, out: str = OUT, define
     sys.path.insert(0, CSRC)
     try:
         import gen_bwd_pipe
+        import gen_dq_pipe
         import gen_fwd_pipe
         gen_fwd_pipe.main()
         gen_bwd_pipe.main()
+        gen_dq_pipe.main()
     finally:
         sys.path.remove(CSRC)
     objdir = OBJ if not defines else os.path.join(OBJ, "_".join(defines).replace("=", "-"))

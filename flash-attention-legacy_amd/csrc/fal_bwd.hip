@@ -24,6 +24,7 @@
 
 #include "fal_kernels.h"
 #include "fal_bwd_pipe.inc"
+#include "fal_dq_pipe.inc"
 
 namespace fal {
 
@@ -981,8 +982,12 @@ bwd_kv_pipe_kernel(BwdParams p) {
 #ifndef FAL_BWD_DQ_WPE
 #define FAL_BWD_DQ_WPE 2
 #endif
-template <class T, int D, int NW, int BN, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(FAL_BWD_DQ_WPE, 8)))
+#ifndef FAL_BWD_DQ_PIPE
+#define FAL_BWD_DQ_PIPE 1   // batched head_dim 128: software-pipelined key-tile loop (fal_dq_pipe.inc)
+#endif
+template <class T, int D, int NW, int BN, bool CAUSAL, bool PIPE = false>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(PIPE ? 1 : FAL_BWD_DQ_WPE, PIPE ? 1 : 8)))
 bwd_dq_kernel(BwdParams p) {
   using V8 = vec8<T>;
   using V4 = vec4<T>;
@@ -995,8 +1000,11 @@ bwd_dq_kernel(BwdParams p) {
   constexpr int PART = BN * CPR * 8;
   constexpr int IPT = BN * CPR / (NW * 64);
   static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
+  // PIPE (batched, head_dim 128): the key-tile loop is the software-pipelined asm block
+  // of fal_dq_pipe.inc at one wave per SIMD, with a ring of 4 K/V tiles
+  static_assert(!PIPE || (D == 128 && NW == 4 && BN == 64), "the pipelined loop is written for this shape");
 
-  __shared__ __attribute__((aligned(1024))) T smem[2 * 2 * PART];
+  __shared__ __attribute__((aligned(1024))) T smem[(PIPE ? 4 : 2) * 2 * PART];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1122,6 +1130,66 @@ bwd_dq_kernel(BwdParams p) {
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int db = 0; db < DB; ++db) taddr[hf][db] = TL::offset(hf * 8 + rl, db * 4 + cl) + 4 * (lane & 1);
+  }
+
+  if constexpr (PIPE) {
+    // The whole key-tile loop: dQ^T += K^T dS^T of tile j-1, the gradient of tile j and
+    // S^T, dP^T of tile j+1 overlap inside the wave; the masking of the diagonal and
+    // last tiles is done inside.  dQ^T comes back through this wave's 16 KB of LDS.
+    typedef __attribute__((address_space(3))) T lds_t;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_t*)smem);
+    uint32_t p_ka[KS], p_ta[2][DB];
+#pragma unroll
+    for (int t = 0; t < KS; ++t) p_ka[t] = lds0 + 2 * kaddr[t];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) p_ta[hf][db] = lds0 + 2 * taddr[hf][db];
+    const uint32_t p_lbase = __builtin_amdgcn_readfirstlane(lds0 + ws * 64 * 16);
+    const uint32_t p_olds = lds0 + ws * 16384 + lane * 16;
+    const int p_row = CAUSAL ? row : 0x3fffffff;
+    const int p_hh4 = hh * 4;
+    const float p_nl = -lrow2, p_dl = drow;
+    const float p_c = c, p_negc = c > 0.f ? -INFINITY : INFINITY;   // c * negc = -inf
+    const int64_t rows_left = max((int64_t)nk, (int64_t)0);
+    const uint64_t ka0 = (uint64_t)(uintptr_t)kbase, va0 = (uint64_t)(uintptr_t)vbase;
+    const uint32_t pk_rs[4] = {(uint32_t)ka0, (uint32_t)(ka0 >> 32) & 0xffffu,
+                               (uint32_t)min(rows_left * p.k_ss * 2, (int64_t)0x7fffffff), 0x00020000u};
+    const uint32_t pv_rs[4] = {(uint32_t)va0, (uint32_t)(va0 >> 32) & 0xffffu,
+                               (uint32_t)min(rows_left * p.v_ss * 2, (int64_t)0x7fffffff), 0x00020000u};
+    const uint32_t p_ktb = (uint32_t)(BN * p.k_ss * 2), p_vtb = (uint32_t)(BN * p.v_ss * 2);
+    const uint32_t p_krb = (uint32_t)(p.k_ss * 2), p_vrb = (uint32_t)(p.v_ss * 2);
+    const int p_rows = (int)min(rows_left, (int64_t)0x7fffffff);
+    // tiles of this wave: [0, jl]; causal waves stop at their diagonal tile, waves whose
+    // rows are all past the end have none
+    const int wrow0 = m0 + ws * 32;
+    int jl = CAUSAL ? min(ntiles - 1, (wrow0 + 31) / BN) : ntiles - 1;
+    if (wrow0 >= nq) jl = -1;
+    const int p_jl = __builtin_amdgcn_readfirstlane(jl);
+    const int p_jend = ntiles, p_nk = nk;
+    const int p_wrow = CAUSAL ? wrow0 : 0x3fffffff;
+    if (ntiles > 0) {
+      if constexpr (std::is_same<T, half_t>::value)
+        asm volatile(FAL_DQP_ASM_F16 : FAL_DQP_OUTS : FAL_DQP_INS : FAL_DQP_CLOBBERS);
+      else
+        asm volatile(FAL_DQP_ASM_BF16 : FAL_DQP_OUTS : FAL_DQP_INS : FAL_DQP_CLOBBERS);
+    }
+    if (row < nq) {
+      const char* ob = (const char*)smem + ws * 16384 + lane * 16;
+      T* dqrow = (T*)p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)(q_off + row) * p.dq_ss;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          f32x4 x = {0.f, 0.f, 0.f, 0.f};
+          if (ntiles > 0) x = *reinterpret_cast<const f32x4*>(ob + (db * 4 + g4) * 1024);
+          V4 h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (T)(x[e] * p.scale);
+          *reinterpret_cast<V4*>(dqrow + db * 32 + g4 * 8 + hh * 4) = h;
+        }
+    }
+    continue;
   }
 
   auto load_tile = [&](int tile, int buf) {
@@ -1314,6 +1382,15 @@ template <class T, int D>
 static hipError_t launch_bwd_dq_t(const BwdParams& p, int causal, dim3 grid, hipStream_t st) {
   if (!p.cu_q && causal && FAL_BWD_DQ_PAIR)
     grid.x = (unsigned)((cdiv(p.Nq, kDqNW * 32) + 1) / 2) * p.B * p.Hq;
+  if constexpr (D == 128) {
+    if (!p.cu_q && FAL_BWD_DQ_PIPE) {
+      if (causal)
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, kDqNW, 64, true, true>), grid, dim3(kDqNW * 64), 0, st, p);
+      else
+        hipLaunchKernelGGL((bwd_dq_kernel<T, D, kDqNW, 64, false, true>), grid, dim3(kDqNW * 64), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   if (causal)
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, kDqNW, FAL_BWD_DQ_BN, true>), grid, dim3(kDqNW * 64), 0, st, p);
   else
