@@ -97,16 +97,30 @@ def bench_c2(steps, warmup):
     return wall, ev, fwd_flops(B, Hq, N, N, d, True)
 
 
-def bench_extra(steps, warmup):
-    from flash_attn_legacy import hip_ext
+def bench_extra(steps, warmup, which=("c1", "c3", "c4", "c5")):
     out = {}
-    # C1
+    if "c1" in which:
+        bench_c1(out, steps, warmup)
+    if "c3" in which:
+        bench_c3(out, steps, warmup)
+    if "c4" in which:
+        bench_c4(out, steps, warmup)
+    if "c5" in which:
+        bench_c5(out, steps, warmup)
+    return out
+
+
+def bench_c1(out, steps, warmup):
+    from flash_attn_legacy import hip_ext
     q, k, v = (randn((2, 8, 1024, 64), s) for s in (0, 1, 2))
     _, ev = time_steps(lambda: hip_ext.forward(q, k, v, 0.125, True), steps, warmup)
     f = fwd_flops(2, 8, 1024, 1024, 64, True)
     out["c1_fwd"] = {"tflops": round(f / ev / 1e9, 2), "ms": round(ev, 4),
                      "frac_peak": round(f / ev / 1e9 / PEAK_FP16_TFLOPS, 4)}
-    # C3 backward
+
+
+def bench_c3(out, steps, warmup):
+    from flash_attn_legacy import hip_ext
     B, H, N, d = 2, 16, 2048, 128
     q, k, v, do = (randn((B, H, N, d), s) for s in (0, 1, 2, 3))
     scale = 1.0 / math.sqrt(d)
@@ -115,8 +129,11 @@ def bench_extra(steps, warmup):
     f = 2.5 * fwd_flops(B, H, N, N, d, True)
     out["c3_bwd"] = {"tflops": round(f / ev / 1e9, 2), "ms": round(ev, 4),
                      "frac_peak": round(f / ev / 1e9 / PEAK_FP16_TFLOPS, 4)}
-    del q, k, v, do, o, lse
-    # C4 varlen forward
+
+
+def bench_c4(out, steps, warmup):
+    from flash_attn_legacy import hip_ext
+    scale = 1.0 / math.sqrt(128)
     g = torch.Generator().manual_seed(0)
     lens = [int(x) for x in torch.randint(64, 4097, (16,), generator=g)]
     tot = sum(lens)
@@ -127,8 +144,11 @@ def bench_extra(steps, warmup):
     f = sum(fwd_flops(1, 32, n, n, 128, True) for n in lens)
     out["c4_varlen_fwd"] = {"tflops": round(f / ev / 1e9, 2), "ms": round(ev, 4),
                             "frac_peak": round(f / ev / 1e9 / PEAK_FP16_TFLOPS, 4), "total_tokens": tot}
-    del q, k, v
-    # C5 decode
+
+
+def bench_c5(out, steps, warmup):
+    from flash_attn_legacy import hip_ext
+    scale = 1.0 / math.sqrt(128)
     g = torch.Generator().manual_seed(0)
     lens = [int(x) for x in torch.randint(1024, 32769, (32,), generator=g)]
     S = max(lens)
@@ -139,7 +159,6 @@ def bench_extra(steps, warmup):
     nbytes = sum(lens) * 8 * 128 * 2 * 2
     out["c5_decode"] = {"gbs": round(nbytes / ev / 1e6, 1), "ms": round(ev, 4),
                         "frac_peak": round(nbytes / ev / 1e6 / PEAK_HBM_GBS, 4), "kv_bytes": nbytes}
-    return out
 
 
 # Packed-vs-padded scenarios of the reference's varlen benchmark
@@ -275,9 +294,11 @@ def main():
     ap.add_argument("--prerun-s", type=float, default=2.0,
                     help="seconds of untimed calls of the workload right before its warmup (clock "
                          "settling); the extra workloads get a quarter of it each")
-    ap.add_argument("--only", choices=["c2", "all", "copy"], default="all",
+    ap.add_argument("--only", choices=["c2", "all", "copy", "c1", "c3", "c4", "c5"], default="all",
                     help="c2: the headline line without the extra configurations; copy: a 1 GiB "
-                         "device copy only, the known-size kernel that calibrates HBM byte counters")
+                         "device copy only, the known-size kernel that calibrates HBM byte counters; "
+                         "c1/c3/c4/c5: that one extra workload alone (for profiler runs), printed as "
+                         "{\"extra\": ...}")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -297,6 +318,9 @@ def main():
 
     global PRERUN_S
     PRERUN_S = max(a.prerun_s, 0.0)
+    if a.only in ("c1", "c3", "c4", "c5"):
+        print(json.dumps({"extra": bench_extra(a.steps, a.warmup, (a.only,))}), flush=True)
+        return
     wall, ev, flops = bench_c2(a.steps, a.warmup)
     value = flops / (wall * 1e-3) / 1e12
     achieved = flops / (ev * 1e-3) / 1e12
