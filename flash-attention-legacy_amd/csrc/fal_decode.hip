@@ -38,6 +38,35 @@ namespace fal {
 #ifndef FAL_DEC_VAUX
 #define FAL_DEC_VAUX 2   // cache-policy bits of the V loads: nt (read once, evict first)
 #endif
+// K rows loaded a whole 128-byte line per instruction (8 rows x 128 B, both halves of a
+// pair of MFMA k-steps), swapped into the MFMA layout with two row_ror:8 DPP moves per
+// dword, so the K loads can carry the nontemporal bit too (a half-line load with nt
+// drops the line before the next instruction reads its other half).
+#ifndef FAL_DEC_KLINE
+#define FAL_DEC_KLINE 1
+#endif
+#ifndef FAL_DEC_KAUX
+#define FAL_DEC_KAUX (FAL_DEC_KLINE ? 2 : 0)
+#endif
+
+// A pair of K loads in line order -> MFMA order.  Loaded: a = (lane n < 8: row n chunk g;
+// n >= 8: row n-8 chunk 4+g), b = (n < 8: row n+8 chunk g; n >= 8: row n chunk 4+g)
+// for lane 16g + n.  Wanted: a = row n chunk g, b = row n chunk 4+g.  Lanes 8-15 of
+// each 16-lane row take b from 8 lanes below, lanes 0-7 take a from 8 lanes above
+// (row_ror:8; bank_mask selects 4-lane banks).
+template <class V8>
+__device__ __forceinline__ void kline_unswap(V8& a, V8& b) {
+  auto ua = __builtin_bit_cast(u32x4, a);
+  auto ub = __builtin_bit_cast(u32x4, b);
+  u32x4 na, nb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    na[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)ua[i], (int)ub[i], 0x128, 0xf, 0xc, false);
+    nb[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)ub[i], (int)ua[i], 0x128, 0xf, 0x3, false);
+  }
+  a = __builtin_bit_cast(V8, na);
+  b = __builtin_bit_cast(V8, nb);
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
@@ -147,8 +176,12 @@ decode_split_kernel(DecodeParams p) {
 
   const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
   const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
-  // K: lane loads row l16, columns t*32 + g4*8 .. +8 of each slice (A operand layout)
+  // K: lane loads row l16, columns t*32 + g4*8 .. +8 of each slice (A operand layout);
+  // with FAL_DEC_KLINE a pair of k-steps (t, t+1) is loaded as whole lines instead
+  // (kline_unswap restores the layout)
   const int kvo = (int)(l16 * p.k_ss + g4 * 8) * 2;
+  const int kvl = (int)((l16 & 7) * p.k_ss + (g4 + 4 * (l16 >> 3)) * 8) * 2;
+  const int kvl8 = kvl + (int)(8 * p.k_ss) * 2;
   // V: load instruction I of a slice fills chunks [I*64, I*64+64)
   int vvo[VI];
 #pragma unroll
@@ -173,8 +206,16 @@ decode_split_kernel(DecodeParams p) {
       const __amdgpu_buffer_rsrc_t vrs =
           make_rsrc(vbase + (int64_t)rs * p.v_ss, (uint32_t)min(left * p.v_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
-      for (int t = 0; t < KS; ++t)
-        kreg[buf][sl][t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo + t * 64, 0, 0));
+      for (int t = 0; t < KS; ++t) {
+        if (FAL_DEC_KLINE && (t & 1) == 0 && t + 1 < KS)
+          kreg[buf][sl][t] = __builtin_bit_cast(
+              V8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvl + t * 64, 0, FAL_DEC_KAUX));
+        else if (FAL_DEC_KLINE && (t & 1) == 1)
+          kreg[buf][sl][t] = __builtin_bit_cast(
+              V8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvl8 + (t - 1) * 64, 0, FAL_DEC_KAUX));
+        else
+          kreg[buf][sl][t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo + t * 64, 0, 0));
+      }
 #pragma unroll
       for (int I = 0; I < VI; ++I)
         buffer_to_lds16<FAL_DEC_VAUX>(vrs, vvo[I], vring + (buf * 2 + sl) * SLICE + I * 64 * 8);
@@ -216,6 +257,10 @@ decode_split_kernel(DecodeParams p) {
     f32x4 s[2];
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
+      if (FAL_DEC_KLINE) {
+#pragma unroll
+        for (int t = 0; t + 1 < KS; t += 2) kline_unswap(kreg[buf][sl][t], kreg[buf][sl][t + 1]);
+      }
       s[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < KS; ++t) s[sl] = mfma16(kreg[buf][sl][t], qreg[t], s[sl]);
