@@ -148,7 +148,12 @@ static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, fl
     p.part_o = static_cast<float*>(workspace);
     p.part_ml = p.part_o + (size_t)batch * heads_q * p.nsplit * seqlen_q * head_dim;
   }
-  const int64_t nblocks = (int64_t)p.n_qtiles * batch * heads_q * p.nsplit;
+  int64_t nblocks = (int64_t)p.n_qtiles * batch * heads_q * p.nsplit;
+  if (!p.kchunk && fwd_gqa4_ok((int)head_dim, heads_q, heads_kv)) {
+    p.gqa4 = 1;
+    p.n_qtiles = cdiv((int)seqlen_q, 64);
+    nblocks = (int64_t)p.n_qtiles * batch * (heads_q / 4);
+  }
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), st);

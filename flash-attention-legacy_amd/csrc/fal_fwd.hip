@@ -125,13 +125,15 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm
     it.split = id % p.nsplit;   // the splits of a query tile run next to each other
     id /= p.nsplit;
     const int g = p.Hq / p.Hkv;
-    const int hg = id % g;
-    int rest = id / g;
+    const int ng = p.gqa4 ? g / 4 : g;           // workgroups per (KV head, query tile)
+    const int hg = id % ng;
+    int rest = id / ng;
     const int t = rest % p.n_qtiles;
     rest /= p.n_qtiles;                          // = b * Hkv + hkv
     it.qt = CAUSAL ? (p.n_qtiles - 1 - t) : t;   // heaviest causal tiles first
     it.b = rest / p.Hkv;
-    it.hq = (rest % p.Hkv) * g + hg;
+    // gqa4: wave w takes query head 4*hg + w of the group
+    it.hq = __builtin_amdgcn_readfirstlane((rest % p.Hkv) * g + (p.gqa4 ? hg * 4 + (int)(threadIdx.x >> 6) : hg));
     it.q_off = 0;
     it.k_off = 0;
     it.nq = p.Nq;
@@ -178,7 +180,10 @@ fwd_kernel(FwdParams p) {
   if (!fwd_item<CAUSAL>(p, it, BM)) return;
   const int b = it.b, hq = it.hq, qt = it.qt, q_off = it.q_off, k_off = it.k_off, nq = it.nq, nk = it.nk;
   const int hkv = hq / (p.Hq / p.Hkv);
-  const int m0 = qt * BM;
+  // gqa4 (pipelined loop only): the waves share 64 query rows of different heads
+  const bool gqa4 = PIPE && p.gqa4;
+  const int BMW = gqa4 ? 32 * RB : BM;      // query rows per workgroup and head
+  const int m0 = qt * BMW;
   if (m0 >= nq) return;
 
   const T* qbase = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
@@ -199,7 +204,7 @@ fwd_kernel(FwdParams p) {
   V8 qreg[RB][KS];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    row[rb] = m0 + (w * RB + rb) * 32 + l32;
+    row[rb] = m0 + ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       V8 x = row[rb] < nq ? ld8(qbase + (int64_t)row[rb] * p.q_ss + t * 16 + hh * 8) : zero8<T>();
@@ -216,7 +221,7 @@ fwd_kernel(FwdParams p) {
   }
 
   // ---- key range: tiles [jbeg, jend), the whole range or this workgroup's split ----
-  const int kend = CAUSAL ? min(nk, m0 + BM) : nk;
+  const int kend = CAUSAL ? min(nk, m0 + BMW) : nk;
   int jbeg = 0, jend = cdiv(kend, BN);
   if (p.kchunk) {
     jbeg = it.split * p.kchunk;
@@ -475,7 +480,7 @@ fwd_kernel(FwdParams p) {
     const int p_rows = (int)rows_left;
     // tiles of this wave: [jbeg, jl]; causal waves stop at their diagonal tile, waves
     // whose rows are all past the sequence have none
-    const int wrow0 = m0 + ws * RB * 32;
+    const int wrow0 = m0 + (gqa4 ? 0 : ws) * RB * 32;
     int jl = CAUSAL ? min(jend - 1, (wrow0 + RB * 32 - 1) / BN) : jend - 1;
     if (wrow0 >= nq) jl = jbeg - 1;
     const int p_jl = __builtin_amdgcn_readfirstlane(jl);
@@ -873,6 +878,16 @@ hipError_t launch_fwd_combine(const FwdParams& p, int d, int causal, hipStream_t
     case 256: return launch_combine_d<256>(p, causal, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+#ifndef FAL_FWD_GQA4
+#define FAL_FWD_GQA4 1
+#endif
+// True when a batched (not split) forward of this head dim and head ratio runs the
+// pipelined kernel with the four-heads-per-workgroup layout (FwdParams::gqa4).
+bool fwd_gqa4_ok(int d, int64_t heads_q, int64_t heads_kv) {
+  return FAL_FWD_GQA4 && FAL_FWD_PIPE && !FAL_PRESCALE_FP16 && d == 128 && FwdCfg<128>::RB == 2 &&
+         FwdCfg<128>::NW == 4 && FwdCfg<128>::BN == 64 && heads_kv > 0 && (heads_q / heads_kv) % 4 == 0;
 }
 
 int fwd_block_m(int d) {

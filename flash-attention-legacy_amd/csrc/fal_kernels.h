@@ -40,6 +40,11 @@ struct FwdParams {
   int nsplit;         // splits per query tile (grid = B * Hq * n_qtiles * nsplit)
   float* part_o;      // [B * Hq * nsplit, Nq, d] fp32
   float* part_ml;     // [B * Hq * nsplit, Nq, 2]: log2-domain max m and sum l (true sum 2^m * l)
+  // Batched head_dim-128 pipelined kernel with Hq/Hkv a multiple of 4: the four waves of
+  // a workgroup take the same 64 query rows of four query heads that share one KV head
+  // (n_qtiles counts 64-row tiles, the grid B * Hq/4 * n_qtiles), so under a causal mask
+  // every wave stops at the same diagonal tile.
+  int gqa4;
 };
 
 // Backward.  Same addressing as FwdParams, plus dO (do_*), the fp32 dQ
@@ -108,6 +113,7 @@ struct DecodeParams {
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 int fwd_block_m(int d);
+bool fwd_gqa4_ok(int d, int64_t heads_q, int64_t heads_kv);   // FwdParams::gqa4 applies
 int fwd_block_m_varlen(int d);   // query rows per workgroup of a packed-sequence call
 int fwd_block_n(int d);
 // Split-KV plan for a batched forward: sets kchunk / nsplit (kchunk 0 = no split) and
