@@ -4,6 +4,7 @@
 // it validates shapes, strides and alignment, lays out the caller-provided
 // workspace, fills the kernel parameter blocks and enqueues the kernels on the
 // caller's stream.  It never allocates device memory and never synchronises.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -103,6 +104,21 @@ size_t fal_fwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, 
   return fwd_split_plan(batch, heads_q, seqlen_q, seqlen_k, (int)head_dim, is_causal != 0, &kchunk, &nsplit);
 }
 
+#ifndef FAL_FWD_PERSIST
+#define FAL_FWD_PERSIST 1
+#endif
+// Compute units of the current device (cached per device; 0 if the query fails).
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cached[dev] = n;
+  return n;
+}
+
 static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
             int64_t heads_q, int64_t heads_kv, int64_t seqlen_q, int64_t seqlen_k, int64_t head_dim,
             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
@@ -153,6 +169,13 @@ static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, fl
     p.gqa4 = 1;
     p.n_qtiles = cdiv((int)seqlen_q, 64);
     nblocks = (int64_t)p.n_qtiles * batch * (heads_q / 4);
+    // at least two items per CU: one persistent workgroup per CU walks pairs of tiles
+    const int ncu = device_cu_count();
+    if (FAL_FWD_PERSIST && ncu > 0 && nblocks >= 2 * (int64_t)ncu) {
+      p.persist = 1;
+      const int64_t pairs = (int64_t)(p.n_qtiles + 1) / 2 * batch * (heads_q / 4);
+      nblocks = std::min<int64_t>(pairs, ncu);
+    }
   }
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
   hipStream_t st = static_cast<hipStream_t>(stream);

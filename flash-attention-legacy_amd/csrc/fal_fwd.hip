@@ -53,6 +53,7 @@ namespace fal {
 // A workgroup's (batch or sequence, query head, query tile) and its row ranges.
 struct FwdItem {
   int b, hq, qt, q_off, k_off, nq, nk, split;
+  int pre;   // persistent schedule: copies of the first two K/V tiles already issued (2) or not (0)
 };
 
 // Item `item` of the varlen forward work list for at most 64 sequences, derived in the
@@ -89,6 +90,7 @@ __device__ __forceinline__ bool varlen_item_small(const int* cu, int num_seqs, i
 // padding block, which exits.
 template <bool CAUSAL>
 __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm) {
+  it.pre = 0;
   if (p.cu_q) {
     // 1-D grid over (work item, KV head) groups of G query heads.  Block i runs on XCD
     // i % 8 as that XCD's (i / 8)-th block; the groups are dealt to the XCDs round-robin
@@ -142,10 +144,13 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm
   return true;
 }
 
+// One work item (query tile of one head, or of four heads under gqa4) of fwd_kernel.
+// Every wave of the workgroup takes the same early returns.
+// Returns 2 when it issued the copies of the next item's first two K/V tiles (persistent
+// schedule; `next` is valid when has_next), else 0.
 template <class T, int D, int NW, int BN, bool CAUSAL, int RB>
-__global__ void __launch_bounds__(NW * 64)
-__attribute__((amdgpu_waves_per_eu((RB == 2 && D >= 128) ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
-fwd_kernel(FwdParams p) {
+__device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T* smem, const FwdItem& next,
+                                        bool has_next) {
   using TL = SwizzledTile<D>;
   using V8 = vec8<T>;
   using V4 = vec4<T>;
@@ -166,25 +171,29 @@ fwd_kernel(FwdParams p) {
   constexpr int IPT = BN * CPR / (NW * 64);   // direct-to-LDS loads per wave per part
   static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
 
-  constexpr int NSLOT = PIPE ? 4 : 2;
-  __shared__ __attribute__((aligned(1024))) T smem[NSLOT * 2 * PART];
-
-  const int tid = threadIdx.x;
+  // (an opaque copy: under the persistent schedule the per-lane addresses below are
+  // recomputed per item instead of being hoisted out of the item loop and kept live,
+  // spilled, across the asm block)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
+  int pre_next = 0;
 
-  // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
-  FwdItem it;
-  if (!fwd_item<CAUSAL>(p, it, BM)) return;
   const int b = it.b, hq = it.hq, qt = it.qt, q_off = it.q_off, k_off = it.k_off, nq = it.nq, nk = it.nk;
   const int hkv = hq / (p.Hq / p.Hkv);
   // gqa4 (pipelined loop only): the waves share 64 query rows of different heads
   const bool gqa4 = PIPE && p.gqa4;
+#ifdef FAL_FWD_WGSTAMP
+  // measurement build: per-workgroup s_memrealtime stamps into the L buffer (L is not written)
+  const uint32_t st0 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+  uint32_t st1 = 0;
+#endif
   const int BMW = gqa4 ? 32 * RB : BM;      // query rows per workgroup and head
   const int m0 = qt * BMW;
-  if (m0 >= nq) return;
+  if (m0 >= nq) return 0;
 
   const T* qbase = (const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq * p.q_sh + (int64_t)q_off * p.q_ss;
   const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)k_off * p.k_ss;
@@ -226,7 +235,7 @@ fwd_kernel(FwdParams p) {
   if (p.kchunk) {
     jbeg = it.split * p.kchunk;
     jend = min(jend, jbeg + p.kchunk);
-    if (jbeg >= jend && it.split > 0) return;   // split past this tile's keys (split 0 always reports)
+    if (jbeg >= jend && it.split > 0) return 0;   // split past this tile's keys (split 0 always reports)
   }
   // tiles below this index need no masking for any row of the workgroup
   const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
@@ -466,9 +475,12 @@ fwd_kernel(FwdParams p) {
     const int p_hh4 = hh * 4;
     // copy resources of tile jbeg over the rows [jbeg*BN, min(nk, jend*BN)); each copy
     // advances them by one tile, so rows past that range read as zeros
-    const int64_t rows_left = max((int64_t)min(nk, jend * BN) - (int64_t)jbeg * BN, (int64_t)0);
-    const uint64_t ka0 = (uint64_t)(uintptr_t)(kbase + (int64_t)jbeg * BN * p.k_ss);
-    const uint64_t va0 = (uint64_t)(uintptr_t)(vbase + (int64_t)jbeg * BN * p.v_ss);
+    // (persistent schedule: with it.pre = 2 the previous item issued the copies of tiles
+    // jbeg and jbeg+1 into slots 0 and 1, and the loop starts copying at jbeg + 2)
+    const int p_npre = __builtin_amdgcn_readfirstlane(it.pre);
+    const int64_t rows_left = max((int64_t)min(nk, jend * BN) - (int64_t)(jbeg + p_npre) * BN, (int64_t)0);
+    const uint64_t ka0 = (uint64_t)(uintptr_t)(kbase + (int64_t)(jbeg + p_npre) * BN * p.k_ss);
+    const uint64_t va0 = (uint64_t)(uintptr_t)(vbase + (int64_t)(jbeg + p_npre) * BN * p.v_ss);
     const uint32_t pk_rs[4] = {(uint32_t)ka0, (uint32_t)(ka0 >> 32) & 0xffffu,
                                (uint32_t)min(rows_left * p.k_ss * 2, (int64_t)0x7fffffff), 0x00020000u};
     const uint32_t pv_rs[4] = {(uint32_t)va0, (uint32_t)(va0 >> 32) & 0xffffu,
@@ -493,12 +505,15 @@ fwd_kernel(FwdParams p) {
       asm volatile(FAL_PIPE_ASM_F16 : FAL_PIPE_OUTS : FAL_PIPE_INS : FAL_PIPE_CLOBBERS);
     else
       asm volatile(FAL_PIPE_ASM_BF16 : FAL_PIPE_OUTS : FAL_PIPE_INS : FAL_PIPE_CLOBBERS);
+#ifdef FAL_FWD_WGSTAMP
+    st1 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+#endif
     const char* ob = (const char*)smem + ws * 32768 + lane * 16;
 #ifdef FAL_PIPE_DEBUG_CYC
     if (lane == 0 && m0 == 0 && hq == 0 && b == 0) {
       // debug build: per-wave cycle sums (PV phase, wait + barrier, S phase, iterations)
       for (int i = 0; i < 4; ++i) obase[ws * 4 + i] = (T)((float)p_dbg[i] / (i < 3 ? 1024.f : 1.f));
-      return;
+      return 0;
     }
 #endif
 #pragma unroll
@@ -511,6 +526,7 @@ fwd_kernel(FwdParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) oacc[rb][db][g4 * 4 + e] = x[e];
         }
+    if (p.persist) __syncthreads();   // every wave has its O out of LDS (the next item reuses it)
   } else {
   if (jbeg < jend) load_tile(jbeg, 0);
   // Tiles that need no mask for any row of the workgroup: straight-line, unrolled by
@@ -556,7 +572,7 @@ fwd_kernel(FwdParams p) {
         if (hh == 0) *reinterpret_cast<float2*>(p.part_ml + prow * 2) = make_float2(m_run[rb], l_tot);
       }
     }
-    return;
+    return 0;
   }
 
   // ---- epilogue: normalise, write O and L ----
@@ -575,13 +591,116 @@ fwd_kernel(FwdParams p) {
           for (int e = 0; e < 4; ++e) h[e] = (T)(oacc[rb][db][g4 * 4 + e] * inv);
           *reinterpret_cast<V4*>(orow + db * 32 + g4 * 8 + hh * 4) = h;
         }
+#ifndef FAL_FWD_WGSTAMP
       if (hh == 0) {
         float L = -INFINITY;
         if (l_tot > 0.f) L = (m_run[rb] + fast_log2(l_tot)) * kLn2;
         lbase[(int64_t)row[rb] * p.l_ss] = L;
       }
+#endif
     }
   }
+  // Persistent schedule: the next item's first two K/V tiles go into slots 0 and 1 (the
+  // copies the loop's prologue would issue) after this item's O stores, so their latency
+  // overlaps those stores and the next item's Q loads.
+  if (PIPE && p.persist && has_next && next.qt * BMW < next.nq) {
+    const int nm0 = next.qt * BMW;
+    const int nkend = CAUSAL ? min(next.nk, nm0 + BMW) : next.nk;
+    const int njend = cdiv(nkend, BN);
+    if (njend >= 2) {
+      const int nhkv = next.hq / (p.Hq / p.Hkv);
+      const T* nkb = (const T*)p.k + (int64_t)next.b * p.k_sb + (int64_t)nhkv * p.k_sh;
+      const T* nvb = (const T*)p.v + (int64_t)next.b * p.v_sb + (int64_t)nhkv * p.v_sh;
+      const int64_t nrows = min(next.nk, njend * BN);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int64_t rt = min(max(nrows - (int64_t)t * BN, (int64_t)0), (int64_t)BN);
+        const __amdgpu_buffer_rsrc_t krs = make_rsrc(nkb + (int64_t)t * BN * p.k_ss, (uint32_t)(rt * p.k_ss * 2));
+        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(nvb + (int64_t)t * BN * p.v_ss, (uint32_t)(rt * p.v_ss * 2));
+        T* kdst = smem + t * 2 * PART;
+#pragma unroll
+        for (int i = 0; i < IPT; ++i) {
+          const int I = i * NW + ws;
+          buffer_to_lds16(krs, kvo[i], kdst + I * 64 * 8);
+          buffer_to_lds16(vrs, vvo[i], kdst + PART + I * 64 * 8);
+        }
+      }
+      pre_next = 2;
+    }
+  }
+#ifdef FAL_FWD_WGSTAMP
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const uint32_t st2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+  if (lane == 0) {
+    uint32_t hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    uint32_t* dst = reinterpret_cast<uint32_t*>(p.lse) + ((int64_t)blockIdx.x * 4 + w) * 4;
+    dst[0] = st0; dst[1] = st1; dst[2] = st2; dst[3] = (hw & 0xffff) | (xcc << 16);
+  }
+#endif
+  return pre_next;
+}
+
+// Persistent schedule (pipelined head_dim-128 kernel under gqa4, batched calls with at
+// least two items per CU): a grid of one workgroup per CU walks pairs of query tiles,
+// (T-1-p, p) under a causal mask so every pair costs the same, (2p, 2p+1) without.  The
+// pairs are numbered unit-major (unit = batch, KV head, group of four query heads) and
+// round r gives workgroup w pair r*G + w', w' the XCD-major rank of w, so the
+// workgroups of one XCD work on neighbouring pairs of one unit (shared K/V in that
+// XCD's L2).  Between items no workgroup ends: the previous item's O stores are still
+// in flight while the next item's Q and first K/V tiles load.
+template <bool CAUSAL>
+__device__ __forceinline__ bool fwd_item_persist(const FwdParams& p, FwdItem& it, int i) {
+  const int G = gridDim.x, w = blockIdx.x;
+  const int wr = (G & 7) == 0 ? (w & 7) * (G >> 3) + (w >> 3) : w;
+  const int T = p.n_qtiles;
+  const int npair = (T + 1) >> 1;
+  const int g = p.Hq / p.Hkv, ng = g >> 2;
+  // (the host keeps B * Hkv * ng * npair below 2^31)
+  const uint32_t e = (uint32_t)(i >> 1) * (uint32_t)G + (uint32_t)wr;
+  if (e >= (uint32_t)(p.B * p.Hkv * ng * npair)) return false;
+  const int u = (int)(e / (uint32_t)npair), pp = (int)(e % (uint32_t)npair);
+  const int half = i & 1;
+  it.qt = CAUSAL ? (half ? pp : T - 1 - pp) : 2 * pp + half;
+  if (CAUSAL && half && pp == T - 1 - pp) it.qt = T;   // odd T: the middle tile has no partner
+  const int hg = (int)((uint32_t)u % (uint32_t)ng), bh = (int)((uint32_t)u / (uint32_t)ng);
+  it.b = (int)((uint32_t)bh / (uint32_t)p.Hkv);
+  it.hq = __builtin_amdgcn_readfirstlane((bh - it.b * p.Hkv) * g + hg * 4 + (int)(threadIdx.x >> 6));
+  it.q_off = 0;
+  it.k_off = 0;
+  it.nq = p.Nq;
+  it.nk = p.Nk;
+  it.split = 0;
+  it.pre = 0;
+  return true;
+}
+
+template <class T, int D, int NW, int BN, bool CAUSAL, int RB>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu((RB == 2 && D >= 128) ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
+fwd_kernel(FwdParams p) {
+  constexpr bool PIPE = FAL_FWD_PIPE && D == 128 && RB == 2 && NW == 4 && BN == 64 && !FAL_PRESCALE_FP16;
+  constexpr int PART = BN * SwizzledTile<D>::CPR * 8;
+  constexpr int NSLOT = PIPE ? 4 : 2;
+  __shared__ __attribute__((aligned(1024))) T smem[NSLOT * 2 * PART];
+  FwdItem it;
+  if (PIPE && p.persist) {
+    // items past the tile count (qt >= n_qtiles) are skipped inside fwd_body; each item
+    // ends with a barrier after its O left LDS and may issue the next item's first copies
+    FwdItem nx;
+    bool have = fwd_item_persist<CAUSAL>(p, it, 0);
+    for (int i = 0; have; ++i) {
+      const bool more = fwd_item_persist<CAUSAL>(p, nx, i + 1);
+      nx.pre = fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, nx, more);
+      it = nx;
+      have = more;
+    }
+    return;
+  }
+  // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
+  if (!fwd_item<CAUSAL>(p, it, NW * 32 * RB)) return;
+  fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, it, false);
 }
 
 // ---------------------------------------------------------------------------

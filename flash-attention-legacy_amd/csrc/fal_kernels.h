@@ -45,6 +45,8 @@ struct FwdParams {
   // (n_qtiles counts 64-row tiles, the grid B * Hq/4 * n_qtiles), so under a causal mask
   // every wave stops at the same diagonal tile.
   int gqa4;
+  // gqa4 only: persistent grid (one workgroup per CU walking pairs of query tiles)
+  int persist;
 };
 
 // Backward.  Same addressing as FwdParams, plus dO (do_*), the fp32 dQ

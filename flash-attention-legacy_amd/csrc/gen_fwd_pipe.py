@@ -97,7 +97,7 @@ for i in range(4):
 INS += [("c", "s", "c"), ("jbeg", "s", "p_jbeg"), ("jend", "s", "p_jend"), ("jl", "s", "p_jl"),
         ("wrow", "s", "p_wrow"), ("nk", "s", "p_nk"), ("ktb", "s", "p_ktb"), ("vtb", "s", "p_vtb"),
         ("krb", "s", "p_krb"), ("vrb", "s", "p_vrb"), ("rows", "s", "p_rows"),
-        ("lbase", "s", "p_lbase")]
+        ("lbase", "s", "p_lbase"), ("npre", "s", "p_npre")]
 # FAL_PIPE_DEBUG=CYC: per-wave cycle sums of the iteration phases; =S: raw scores of the
 # first tile instead of O
 DEBUG = os.environ.get("FAL_PIPE_DEBUG") if MEASURE else None
@@ -482,8 +482,16 @@ class Emitter:
         for rb in range(2):
             e(f"v_cmp_eq_f32 vcc, {NEG_INF}, {op(f'm{rb}')}")
             e(f"v_cndmask_b32_e64 {v(NM[rb])}, -{op(f'm{rb}')}, 0, vcc")
+        # the first two tiles, unless the caller already issued their copies (npre = 2:
+        # the copy resources, the row count and the tile index then start two tiles on)
+        e(f"s_cmp_eq_u32 {op('npre')}, 0")
+        e(f"s_cbranch_scc0 {L('pre', shared=True)}")
         self.dma()
         self.dma()
+        e(f"s_branch {L('predone', shared=True)}")
+        e(f"{L('pre', shared=True)}:")
+        e(f"s_add_u32 s{SD}, s{SD}, {op('npre')}")
+        e(f"{L('predone', shared=True)}:")
         e("s_waitcnt vmcnt(8)")
         e("s_barrier")
         # S of the first tile (if this wave has any tile), masked, then the first max

@@ -285,3 +285,34 @@ def test_head_slice_beyond_2gib():
         ref_o, ref_l = exact_rows(q[0, h], kv[0, h], vv[0, h], rows, scale, False)
         assert max_abs(o[0, h, rows], torch.from_numpy(ref_o)) <= FWD_ATOL, h
         assert float(np.abs(lse[0, h, rows].cpu().numpy() - ref_l).max()) <= 1e-3, h
+
+
+def _gpu_fp32_attention(q, k, v, scale, causal):
+    """fp32 softmax(QK^T*scale + top-left mask)V of one KV group on the GPU (the same
+    formula as oracle/torch_ref.py; used where the CPU formula would take minutes)."""
+    reps = q.shape[1] // k.shape[1]
+    k, v = k.repeat_interleave(reps, dim=1), v.repeat_interleave(reps, dim=1)
+    s = torch.matmul(q.float(), k.float().transpose(-2, -1)) * scale
+    if causal:
+        n_q, n_k = q.shape[-2], k.shape[-2]
+        s.masked_fill_(torch.triu(torch.ones(n_q, n_k, dtype=torch.bool, device=q.device), 1), float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v.float())
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,N", [(2, 16, 4, 4160), (1, 32, 4, 4160), (2, 8, 2, 8192)])
+def test_persistent_grid_every_head(B, Hq, Hkv, N, causal):
+    """head_dim 128 with Hq/Hkv a multiple of 4 and at least two 64-row items per CU runs
+    the persistent grid (pairs of query tiles per workgroup, an odd tile count leaves the
+    middle tile unpaired): every output row of every head against the fp32 formula."""
+    d = 128
+    scale = 1.0 / math.sqrt(d)
+    q, k, v = randn((B, Hq, N, d), seed=21), randn((B, Hkv, N, d), seed=22), randn((B, Hkv, N, d), seed=23)
+    o, lse = ext().forward(q, k, v, scale, causal)
+    G = Hq // Hkv
+    for b in range(B):
+        for g in range(Hkv):
+            hs = slice(g * G, (g + 1) * G)
+            ref = _gpu_fp32_attention(q[b:b + 1, hs], k[b:b + 1, g:g + 1], v[b:b + 1, g:g + 1], scale, causal)
+            assert float((o[b:b + 1, hs].float() - ref).abs().max()) <= FWD_ATOL, (b, g)
+    assert torch.isfinite(lse).all()
