@@ -609,8 +609,8 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     const int njend = cdiv(nkend, BN);
     if (njend >= 2) {
       const int nhkv = next.hq / (p.Hq / p.Hkv);
-      const T* nkb = (const T*)p.k + (int64_t)next.b * p.k_sb + (int64_t)nhkv * p.k_sh;
-      const T* nvb = (const T*)p.v + (int64_t)next.b * p.v_sb + (int64_t)nhkv * p.v_sh;
+      const T* nkb = (const T*)p.k + (int64_t)next.b * p.k_sb + (int64_t)nhkv * p.k_sh + (int64_t)next.k_off * p.k_ss;
+      const T* nvb = (const T*)p.v + (int64_t)next.b * p.v_sb + (int64_t)nhkv * p.v_sh + (int64_t)next.k_off * p.v_ss;
       const int64_t nrows = min(next.nk, njend * BN);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
