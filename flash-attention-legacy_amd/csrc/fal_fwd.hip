@@ -144,6 +144,11 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm
   return true;
 }
 
+// Pipelined loop's O hand-off in LDS: 32 blocks of 1 KB per wave, 1040 bytes apart so the
+// row-wise reads of the epilogue spread over the banks.
+constexpr int kPipeOStr = 1040;
+constexpr int kPipeOWave = 32 * kPipeOStr;
+
 // One work item (query tile of one head, or of four heads under gqa4) of fwd_kernel.
 // Every wave of the workgroup takes the same early returns.
 // Returns 2 when it issued the copies of the next item's first two K/V tiles (persistent
@@ -181,13 +186,15 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   const int l32 = lane & 31;
   const int hh = lane >> 5;
   int pre_next = 0;
+  bool stored = false;   // the pipelined path wrote O and L itself
 
   const int b = it.b, hq = it.hq, qt = it.qt, q_off = it.q_off, k_off = it.k_off, nq = it.nq, nk = it.nk;
   const int hkv = hq / (p.Hq / p.Hkv);
   // gqa4 (pipelined loop only): the waves share 64 query rows of different heads
   const bool gqa4 = PIPE && p.gqa4;
 #ifdef FAL_FWD_WGSTAMP
-  // measurement build: per-workgroup s_memrealtime stamps into the L buffer (L is not written)
+  // measurement build (wrong results): s_memrealtime stamps per work item (start, tile loop
+  // done, epilogue and next-item copies issued) written over the L buffer
   const uint32_t st0 = (uint32_t)__builtin_amdgcn_s_memrealtime();
   uint32_t st1 = 0;
 #endif
@@ -468,7 +475,7 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
 #pragma unroll
       for (int db = 0; db < DB; ++db) p_va[hf][db] = lds0 + 2 * vaddr[hf][db];
     const uint32_t p_lbase = __builtin_amdgcn_readfirstlane(lds0 + ws * 64 * 16);
-    const uint32_t p_olds = lds0 + ws * 32768 + lane * 16;
+    const uint32_t p_olds = lds0 + ws * kPipeOWave + lane * 16;
     int p_row[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) p_row[rb] = CAUSAL ? row[rb] : 0x3fffffff;
@@ -508,7 +515,9 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
 #ifdef FAL_FWD_WGSTAMP
     st1 = (uint32_t)__builtin_amdgcn_s_memrealtime();
 #endif
-    const char* ob = (const char*)smem + ws * 32768 + lane * 16;
+    // O^T accumulator block g (= (rb*DB + db)*4 + g4) of lane l is at byte
+    // ws*kPipeOWave + l*16 + g*kPipeOStr: 16 bytes of a row (MFMA layout)
+    const char* wbase = (const char*)smem + ws * kPipeOWave;
 #ifdef FAL_PIPE_DEBUG_CYC
     if (lane == 0 && m0 == 0 && hq == 0 && b == 0) {
       // debug build: per-wave cycle sums (PV phase, wait + barrier, S phase, iterations)
@@ -516,16 +525,62 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
       return 0;
     }
 #endif
+    if (p.kchunk) {
+      // split-KV partials: back into the accumulator layout
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(ob + ((rb * DB + db) * 4 + g4) * 1024);
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(wbase + lane * 16 + ((rb * DB + db) * 4 + g4) * kPipeOStr);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) oacc[rb][db][g4 * 4 + e] = x[e];
+            for (int e = 0; e < 4; ++e) oacc[rb][db][g4 * 4 + e] = x[e];
+          }
+    } else {
+      // O and L straight from LDS: each store instruction writes 4 whole rows (16 lanes
+      // x 16 bytes per row), where stores from the accumulator layout would write 16
+      // bytes into each of 32 rows
+      float inv[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const float l_tot = pair_sum(l_run[rb]);
+        inv[rb] = l_tot > 0.f ? 1.f / l_tot : 0.f;
+#ifndef FAL_FWD_WGSTAMP
+        if (hh == 0 && row[rb] < nq)
+          lbase[(int64_t)row[rb] * p.l_ss] = l_tot > 0.f ? (m_run[rb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
+#endif
+      }
+      const int cch = lane & 15;               // 16-byte chunk of the row
+      const int wr0 = m0 + (gqa4 ? 0 : w) * RB * 32;
+      // per row block: all LDS reads and row factors first, then the stores (one wait,
+      // not one per row)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        f32x4 a0[8], a1[8];
+        float iv[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int l32w = jj * 4 + (lane >> 4);
+          const int g = rb * 16 + cch;
+          a0[jj] = *reinterpret_cast<const f32x4*>(wbase + l32w * 16 + g * kPipeOStr);
+          a1[jj] = *reinterpret_cast<const f32x4*>(wbase + (32 + l32w) * 16 + g * kPipeOStr);
+          iv[jj] = __shfl(inv[rb], l32w);
         }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int r = rb * 32 + jj * 4 + (lane >> 4);   // row of the wave, 0..63
+          V8 h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            h[e] = (T)(a0[jj][e] * iv[jj]);
+            h[4 + e] = (T)(a1[jj][e] * iv[jj]);
+          }
+          if (wr0 + r < nq) st_u4(obase + (int64_t)(wr0 + r) * p.o_ss + cch * 8, __builtin_bit_cast(u32x4, h));
+        }
+      }
+      stored = true;
+    }
     if (p.persist) __syncthreads();   // every wave has its O out of LDS (the next item reuses it)
   } else {
   if (jbeg < jend) load_tile(jbeg, 0);
@@ -577,7 +632,7 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
 
   // ---- epilogue: normalise, write O and L ----
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+  for (int rb = 0; rb < RB && !stored; ++rb) {
     const float l_tot = pair_sum(l_run[rb]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (row[rb] < nq) {
@@ -629,14 +684,15 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     }
   }
 #ifdef FAL_FWD_WGSTAMP
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  const uint32_t st2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
-  if (lane == 0) {
-    uint32_t hw, xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    uint32_t* dst = reinterpret_cast<uint32_t*>(p.lse) + ((int64_t)blockIdx.x * 4 + w) * 4;
-    dst[0] = st0; dst[1] = st1; dst[2] = st2; dst[3] = (hw & 0xffff) | (xcc << 16);
+  {
+    const uint32_t st2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+    if (lane == 0 && w == 0) {
+      // one record per item: start, tile loop done, O stored (issued), workgroup
+      const int64_t rec = (int64_t)blockIdx.x * 64 + (it.qt & 63);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(p.lse) + (p.persist ? ((int64_t)(b * p.Hkv + hkv) * (p.Hq / p.Hkv / 4) +
+                          (hq % (p.Hq / p.Hkv)) / 4) * p.n_qtiles + qt : rec) * 4;
+      dst[0] = st0; dst[1] = st1; dst[2] = st2; dst[3] = blockIdx.x;
+    }
   }
 #endif
   return pre_next;
@@ -683,7 +739,9 @@ fwd_kernel(FwdParams p) {
   constexpr bool PIPE = FAL_FWD_PIPE && D == 128 && RB == 2 && NW == 4 && BN == 64 && !FAL_PRESCALE_FP16;
   constexpr int PART = BN * SwizzledTile<D>::CPR * 8;
   constexpr int NSLOT = PIPE ? 4 : 2;
-  __shared__ __attribute__((aligned(1024))) T smem[NSLOT * 2 * PART];
+  // the pipelined loop's O hand-off (4 x kPipeOWave bytes) reaches past the 128 KB ring
+  constexpr int NSMEM = PIPE ? (4 * kPipeOWave) / 2 : NSLOT * 2 * PART;
+  __shared__ __attribute__((aligned(1024))) T smem[NSMEM];
   FwdItem it;
   if (PIPE && p.persist) {
     // items past the tile count (qt >= n_qtiles) are skipped inside fwd_body; each item

@@ -22,8 +22,9 @@ LDS: a ring of 4 slots of 32 KB (K tile 16 KB, then V tile 16 KB), XOR-swizzled 
 SwizzledTile<128>.  Tile t is copied into slot t % 4 by buffer->LDS loads two
 iterations ahead.  One barrier per iteration, after the PV products of tile j-1 and
 before the S products of tile j+1: it publishes tile j+1 and frees the slot of tile
-j-1.  After the last tile the wave writes its O accumulators to LDS (32 KB per wave,
-the ring is free by then) for the C++ epilogue.
+j-1.  After the last tile the wave writes its O accumulators to LDS (32 blocks of 1 KB,
+OSTR bytes apart, from the `olds` address; the ring is free by then) for the C++
+epilogue.
 
 Waves of a workgroup can own different tile ranges (causal: each wave stops at its
 diagonal tile); every wave runs every iteration's copy and barrier, and selects the
@@ -49,6 +50,7 @@ import os
 import sys
 
 NBUF = 4            # LDS ring slots
+OSTR = 1040         # bytes between a wave's O blocks in the LDS hand-off (kPipeOStr in fal_fwd.hip)
 VOFF = 16384        # V offset inside a slot (bytes)
 KDIST = int(os.environ.get("FAL_PIPE_KDIST", "2"))   # K read-ahead (k-steps of 2 fragments)
 VRING = int(os.environ.get("FAL_PIPE_VRING", "4"))   # V^T fragment ring (pairs of transposed reads)
@@ -503,7 +505,7 @@ class Emitter:
             # debug: raw S^T of the first tile to the O hand-off area, l = 1/2 per lane
             e("s_nop 15")
             for g in range(16):
-                e(f"ds_write_b128 {op('olds')}, {vr(SA[0] + 4 * g, 4)} offset:{g * 1024}")
+                e(f"ds_write_b128 {op('olds')}, {vr(SA[0] + 4 * g, 4)} offset:{g * OSTR}")
             e("s_waitcnt lgkmcnt(0)")
             e(f"v_mov_b32 {op('l0')}, 0.5")
             e(f"v_mov_b32 {op('l1')}, 0.5")
@@ -600,7 +602,7 @@ class Emitter:
         e("s_waitcnt vmcnt(0) lgkmcnt(0)")
         e("s_barrier")
         for g in range(32):
-            e(f"ds_write_b128 {op('olds')}, {ar(4 * g, 4)} offset:{g * 1024}")
+            e(f"ds_write_b128 {op('olds')}, {ar(4 * g, 4)} offset:{g * OSTR}")
         e("s_waitcnt lgkmcnt(0)")
         e(f"s_mov_b32 m0, s{SM0}")
         if DBG_CYC:
