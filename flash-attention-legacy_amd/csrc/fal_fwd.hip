@@ -174,6 +174,7 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   constexpr int CPR = TL::CPR;      // 16-byte chunks per row
   constexpr int PART = BN * CPR * 8;          // elements of one K (or V) tile
   constexpr int IPT = BN * CPR / (NW * 64);   // direct-to-LDS loads per wave per part
+  constexpr int NSLOT = PIPE ? 4 : 2;   // K/V tile buffers in LDS
   static_assert(BN * CPR % (NW * 64) == 0, "tile must split evenly over the waves");
 
   // (an opaque copy: under the persistent schedule the per-lane addresses below are
@@ -631,6 +632,44 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   }
 
   // ---- epilogue: normalise, write O and L ----
+  // Through LDS when the tile buffers hold the workgroup's O: each wave stages its rows
+  // (fp16/bf16, rows padded by 16 bytes) and writes them back row-wise, 16 contiguous
+  // bytes per lane, so every store instruction covers whole rows; from the accumulator
+  // layout each store would put 8 bytes into each of 32 rows.
+  constexpr int OROW = D * 2 + 16;
+  constexpr bool ROWST = !PIPE && (NW * RB * 32 * OROW <= NSLOT * 2 * PART * 2);
+  if (ROWST && !stored) {
+    __syncthreads();   // every wave is done with the last K/V tile
+    char* wst = (char*)smem + w * (RB * 32 * OROW);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float l_tot = pair_sum(l_run[rb]);
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          V4 h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (T)(oacc[rb][db][g4 * 4 + e] * inv);
+          *reinterpret_cast<V4*>(wst + (rb * 32 + l32) * OROW + (db * 32 + g4 * 8 + hh * 4) * 2) = h;
+        }
+#ifndef FAL_FWD_WGSTAMP
+      if (hh == 0 && row[rb] < nq)
+        lbase[(int64_t)row[rb] * p.l_ss] = l_tot > 0.f ? (m_run[rb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
+#endif
+    }
+    // (one wave's LDS accesses complete in order: its rows are staged before these reads)
+    constexpr int CPRW = D / 8;
+    const int wr0 = m0 + w * RB * 32;
+#pragma unroll
+    for (int i = lane; i < RB * 32 * CPRW; i += 64) {
+      const int r = i / CPRW, c = i % CPRW;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(wst + r * OROW + c * 16);
+      if (wr0 + r < nq) st_u4(obase + (int64_t)(wr0 + r) * p.o_ss + c * 8, x);
+    }
+    stored = true;
+  }
 #pragma unroll
   for (int rb = 0; rb < RB && !stored; ++rb) {
     const float l_tot = pair_sum(l_run[rb]);
