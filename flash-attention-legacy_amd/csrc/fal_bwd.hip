@@ -827,13 +827,17 @@ bwd2_kernel(BwdParams p) {
 #define FAL_BWD_PIPE 1
 #endif
 constexpr int kPipeBN = 128;    // keys per workgroup
+// dK/dV hand-off in LDS after the loop: per wave, dV then dK*scale, 16 pieces of 512
+// bytes each, kKvOStr apart so the row-wise reads of the epilogue spread over the banks
+constexpr int kKvOStr = 528;
+constexpr int kKvOPart = 16 * kKvOStr;
+constexpr int kKvOWave = 2 * kKvOPart;
 constexpr int kPipeBM = 64;     // query rows per item
 
 template <class T, bool CAUSAL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 bwd_kv_pipe_kernel(BwdParams p) {
   using V8 = vec8<T>;
-  using V4 = vec4<T>;
   using TL = SwizzledTile<128>;
   constexpr int CPR = TL::CPR;
   // 4 slots of (Q tile, dO tile) and 4 slots of (64 Ls, 64 Dn) values
@@ -889,7 +893,7 @@ bwd_kv_pipe_kernel(BwdParams p) {
   }
   const int p_lo4 = lane * 4, p_lo4b = 256 + lane * 4;
   const int p_lk = l32 - 4 * hh;
-  const uint32_t p_olds = lds0 + ws * 16384 + lane * 8;
+  const uint32_t p_olds = lds0 + ws * kKvOWave + lane * 8;
   const uint32_t p_lbase = __builtin_amdgcn_readfirstlane(lds0 + ws * 1024);
   const uint32_t p_ldbase = __builtin_amdgcn_readfirstlane(lds0 + 131072);
   const float p_c = p.scale_log2;
@@ -917,7 +921,6 @@ bwd_kv_pipe_kernel(BwdParams p) {
       vreg[t] = key < nk ? ld8(vbase + (int64_t)key * p.v_ss + t * 16 + hh * 8) : zero8<T>();
     }
     __syncthreads();   // the previous tile's epilogue readers are done with the LDS
-    const char* ob = smem + ws * 16384 + lane * 8;
     if (nitems > 0) {
       const int hq0 = hkv * G;
       const uint64_t qb = (uint64_t)(uintptr_t)((const T*)p.q + (int64_t)b * p.q_sb + (int64_t)hq0 * p.q_sh +
@@ -942,24 +945,33 @@ bwd_kv_pipe_kernel(BwdParams p) {
       else
         asm volatile(FAL_BWDP_ASM_BF16 : FAL_BWDP_OUTS : FAL_BWDP_INS : FAL_BWDP_CLOBBERS);
     }
-    // dV then dK*scale of this wave's keys: piece (db, g4) holds columns
-    // db*32 + g4*8 + hh*4 .. +3 of key `key`
-    if (key < nk) {
-      T* dvrow = (T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + (int64_t)key * p.dv_ss;
-      T* dkrow = (T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + (int64_t)key * p.dk_ss;
+    // dV then dK*scale of this wave's keys: piece pc = db*4 + g4 of lane (hh, l32) holds
+    // columns 8*pc + hh*4 .. +3 of key kw0 + l32, at which*kKvOPart + pc*kKvOStr + lane*8.
+    // Written back row-wise: each 16-byte store instruction covers 4 whole 256-byte rows.
+    {
+      const char* wb = smem + ws * kKvOWave;
+      const int cch = lane & 15;
+      T* dvb = (T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh;
+      T* dkb = (T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh;
 #pragma unroll
-      for (int pc = 0; pc < 16; ++pc) {
-        const int col = (pc >> 2) * 32 + (pc & 3) * 8 + hh * 4;
-        V4 hv, hk;
-        if (nitems > 0) {
-          hv = *reinterpret_cast<const V4*>(ob + pc * 512);
-          hk = *reinterpret_cast<const V4*>(ob + 8192 + pc * 512);
-        } else {
+      for (int which = 0; which < 2; ++which) {
+        u32x4 x[8];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) hv[e] = hk[e] = (T)0.f;
+        for (int jj = 0; jj < 8; ++jj) {
+          const int r = jj * 4 + (lane >> 4);
+          const char* src = wb + which * kKvOPart + cch * kKvOStr;
+          const uint2 lo = *reinterpret_cast<const uint2*>(src + r * 8);
+          const uint2 hi = *reinterpret_cast<const uint2*>(src + (32 + r) * 8);
+          x[jj] = nitems > 0 ? u32x4{lo.x, lo.y, hi.x, hi.y} : u32x4{0u, 0u, 0u, 0u};
         }
-        *reinterpret_cast<V4*>(dvrow + col) = hv;
-        *reinterpret_cast<V4*>(dkrow + col) = hk;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int k = kw0 + jj * 4 + (lane >> 4);
+          if (k < nk) {
+            T* dst = which ? dkb + (int64_t)k * p.dk_ss : dvb + (int64_t)k * p.dv_ss;
+            st_u4(dst + cch * 8, x[jj]);
+          }
+        }
       }
     }
   }
@@ -979,6 +991,10 @@ bwd_kv_pipe_kernel(BwdParams p) {
 #ifndef FAL_BWD_DQ_PAIR
 #define FAL_BWD_DQ_PAIR 1
 #endif
+// pipelined dQ loop's hand-off in LDS: 16 blocks of 1 KB per wave, kDqOStr apart (row-wise
+// reads of the epilogue spread over the banks)
+constexpr int kDqOStr = 1040;
+constexpr int kDqOWave = 16 * kDqOStr;
 #ifndef FAL_BWD_DQ_WPE
 #define FAL_BWD_DQ_WPE 2
 #endif
@@ -1135,7 +1151,7 @@ bwd_dq_kernel(BwdParams p) {
   if constexpr (PIPE) {
     // The whole key-tile loop: dQ^T += K^T dS^T of tile j-1, the gradient of tile j and
     // S^T, dP^T of tile j+1 overlap inside the wave; the masking of the diagonal and
-    // last tiles is done inside.  dQ^T comes back through this wave's 16 KB of LDS.
+    // last tiles is done inside.  dQ^T comes back through this wave's LDS blocks.
     typedef __attribute__((address_space(3))) T lds_t;
     const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_t*)smem);
     uint32_t p_ka[KS], p_ta[2][DB];
@@ -1146,7 +1162,7 @@ bwd_dq_kernel(BwdParams p) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) p_ta[hf][db] = lds0 + 2 * taddr[hf][db];
     const uint32_t p_lbase = __builtin_amdgcn_readfirstlane(lds0 + ws * 64 * 16);
-    const uint32_t p_olds = lds0 + ws * 16384 + lane * 16;
+    const uint32_t p_olds = lds0 + ws * kDqOWave + lane * 16;
     const int p_row = CAUSAL ? row : 0x3fffffff;
     const int p_hh4 = hh * 4;
     const float p_nl = -lrow2, p_dl = drow;
@@ -1174,20 +1190,34 @@ bwd_dq_kernel(BwdParams p) {
       else
         asm volatile(FAL_DQP_ASM_BF16 : FAL_DQP_OUTS : FAL_DQP_INS : FAL_DQP_CLOBBERS);
     }
-    if (row < nq) {
-      const char* ob = (const char*)smem + ws * 16384 + lane * 16;
-      T* dqrow = (T*)p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)(q_off + row) * p.dq_ss;
+    {
+      // dQ^T block g = db*4 + g4 of lane (hh, l32) holds columns 8g + hh*4 .. +3 of row
+      // m0 + ws*32 + l32 at ws*kDqOWave + lane*16 + g*kDqOStr; written back row-wise,
+      // each 16-byte store instruction covering 4 whole rows
+      const char* wb = (const char*)smem + ws * kDqOWave;
+      const int cch = lane & 15;
+      T* dqb = (T*)p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)q_off * p.dq_ss;
+      f32x4 a0[8], a1[8];
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          f32x4 x = {0.f, 0.f, 0.f, 0.f};
-          if (ntiles > 0) x = *reinterpret_cast<const f32x4*>(ob + (db * 4 + g4) * 1024);
-          V4 h;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = (T)(x[e] * p.scale);
-          *reinterpret_cast<V4*>(dqrow + db * 32 + g4 * 8 + hh * 4) = h;
+      for (int jj = 0; jj < 8; ++jj) {
+        const int r = jj * 4 + (lane >> 4);
+        a0[jj] = a1[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (ntiles > 0) {
+          a0[jj] = *reinterpret_cast<const f32x4*>(wb + r * 16 + cch * kDqOStr);
+          a1[jj] = *reinterpret_cast<const f32x4*>(wb + (32 + r) * 16 + cch * kDqOStr);
         }
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int grow = m0 + ws * 32 + jj * 4 + (lane >> 4);
+        V8 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h[e] = (T)(a0[jj][e] * p.scale);
+          h[4 + e] = (T)(a1[jj][e] * p.scale);
+        }
+        if (grow < nq) st_u4(dqb + (int64_t)grow * p.dq_ss + cch * 8, __builtin_bit_cast(u32x4, h));
+      }
     }
     continue;
   }

@@ -20,7 +20,7 @@ and 4 slots of 512 bytes (64 Ls values, 64 Dn values) at 128 KB.  Item F is copi
 into slot F % 4 by buffer->LDS loads two iterations ahead; its Q/dO rows past the end
 of the sequence read as zeros and its Ls rows there hold the value whose exponent is
 -inf, so they add nothing.  After the last item each wave writes dV (fp16/bf16) and
-dK * scale to its own 16 KB of LDS for the C++ epilogue.
+dK * scale to its own pieces of LDS (OSTR apart) for the C++ epilogue.
 
 Causal attention (keys past a row masked): an item whose rows and this wave's keys
 straddle the diagonal gets its scores set to `negc` (c * negc = -inf) before V(i).
@@ -46,6 +46,7 @@ import os
 import sys
 
 NBUF = 4
+OSTR = 528              # bytes between the hand-off pieces (kKvOStr in fal_bwd.hip)
 SLOT = 32768
 DOFF = 16384            # dO tile inside a slot
 LDOFF = 131072          # Ls/Dn slots
@@ -416,7 +417,7 @@ class Emitter:
 
         e(f"{lbl_out}:")
         # every wave is done with the ring: dV and dK*scale (fp16/bf16) to this wave's
-        # 16 KB of LDS, piece (db, g4) of 4 elements at piece*512 + lane*8
+        # LDS, piece (db, g4) of 4 elements at which*16*OSTR + piece*OSTR + lane*8
         e("s_nop 15")
         e("s_nop 15")
         e("s_waitcnt vmcnt(0) lgkmcnt(0)")
@@ -432,7 +433,7 @@ class Emitter:
                             e(f"v_mul_f32 {v(T0 + x)}, {op('scale')}, {v(T0 + x)}")
                     e(f"{self.cvt} {v(T0)}, {v(T0)}, {v(T1)}")
                     e(f"{self.cvt} {v(T1)}, {v(T2)}, {v(T3)}")
-                    e(f"ds_write_b64 {op('olds')}, {vr(T0, 2)} offset:{which * 8192 + (db * 4 + g4) * 512}")
+                    e(f"ds_write_b64 {op('olds')}, {vr(T0, 2)} offset:{which * 16 * OSTR + (db * 4 + g4) * OSTR}")
         e("s_waitcnt lgkmcnt(0)")
         e(f"s_mov_b32 m0, s{SM0}")
         return self.lines

@@ -40,6 +40,7 @@ import os
 import sys
 
 NBUF = 4
+OSTR = 1040             # bytes between the hand-off blocks (kDqOStr in fal_bwd.hip)
 VOFF = 16384
 ADIST = int(os.environ.get("FAL_DQP_ADIST", "4"))   # K/V fragment reads ahead of their MFMA
 QDIST = int(os.environ.get("FAL_DQP_QDIST", "6"))   # transposed reads ahead (2 per MFMA)
@@ -413,13 +414,13 @@ class Emitter:
             self.interleave(reads, mf, QDIST)
             e(f"s_branch {L('out', shared=True)}")
         e(f"{L('out', shared=True)}:")
-        # every wave is done with the ring: dQ^T goes to this wave's 16 KB of LDS
+        # every wave is done with the ring: dQ^T goes to this wave's 16 blocks of LDS, OSTR apart
         for _ in range(2):
             e("s_nop 15")
         e("s_waitcnt vmcnt(0) lgkmcnt(0)")
         e("s_barrier")
         for g in range(16):
-            e(f"ds_write_b128 {op('olds')}, {ar(4 * g, 4)} offset:{g * 1024}")
+            e(f"ds_write_b128 {op('olds')}, {ar(4 * g, 4)} offset:{g * OSTR}")
         e("s_waitcnt lgkmcnt(0)")
         e(f"s_mov_b32 m0, s{SM0}")
         return self.lines
