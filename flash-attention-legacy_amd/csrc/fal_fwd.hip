@@ -209,6 +209,53 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   T* obase = (T*)p.o + (int64_t)b * p.o_sb + (int64_t)hq * p.o_sh + (int64_t)q_off * p.o_ss;
   float* lbase = p.lse + (int64_t)b * p.l_sb + (int64_t)hq * p.l_sh + (int64_t)q_off * p.l_ss;
 
+  // ---- per-lane addressing of the swizzled tiles ----
+  // Load instruction i of wave ws fills LDS chunks [(i*NW + ws)*64, +64) of the tile;
+  // the per-lane global offsets are relative to the tile's first row, so they do not
+  // depend on the tile.
+  const int ws = __builtin_amdgcn_readfirstlane(w);   // wave index as a scalar
+  int kvo[IPT], vvo[IPT];             // byte offsets from the tile's first row
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int I = i * NW + ws;
+    const int pch = I * 64 + lane;
+    const int r = pch / CPR;
+    const int cc = TL::logical_chunk(r, pch % CPR);
+    kvo[i] = (int)(r * p.k_ss + cc * 8) * 2;
+    vvo[i] = (int)(r * p.v_ss + cc * 8) * 2;
+  }
+  // The first two K/V tiles of item x into slots 0 and 1: the copies the pipelined loop's
+  // prologue would issue (it then starts at tile 2).  Returns 2 when issued (x has two
+  // tiles or more), else 0.  Only for the whole key range (no split-KV).
+  auto issue_first2 = [&](const FwdItem& x) -> int {
+    if (!PIPE || p.kchunk) return 0;
+    const int xm0 = x.qt * BMW;
+    if (xm0 >= x.nq) return 0;
+    const int xkend = CAUSAL ? min(x.nk, xm0 + BMW) : x.nk;
+    const int xjend = cdiv(xkend, BN);
+    if (xjend < 2) return 0;
+    const int xhkv = x.hq / (p.Hq / p.Hkv);
+    const T* xkb = (const T*)p.k + (int64_t)x.b * p.k_sb + (int64_t)xhkv * p.k_sh + (int64_t)x.k_off * p.k_ss;
+    const T* xvb = (const T*)p.v + (int64_t)x.b * p.v_sb + (int64_t)xhkv * p.v_sh + (int64_t)x.k_off * p.v_ss;
+    const int64_t xrows = min(x.nk, xjend * BN);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t rt = min(max(xrows - (int64_t)t * BN, (int64_t)0), (int64_t)BN);
+      const __amdgpu_buffer_rsrc_t krs = make_rsrc(xkb + (int64_t)t * BN * p.k_ss, (uint32_t)(rt * p.k_ss * 2));
+      const __amdgpu_buffer_rsrc_t vrs = make_rsrc(xvb + (int64_t)t * BN * p.v_ss, (uint32_t)(rt * p.v_ss * 2));
+      T* kdst = smem + t * 2 * PART;
+#pragma unroll
+      for (int i = 0; i < IPT; ++i) {
+        const int I = i * NW + ws;
+        buffer_to_lds16(krs, kvo[i], kdst + I * 64 * 8);
+        buffer_to_lds16(vrs, vvo[i], kdst + PART + I * 64 * 8);
+      }
+    }
+    return 2;
+  };
+  // this item's first tiles, unless the previous item issued them: in flight with the Q loads
+  const int pre_cur = it.pre ? it.pre : issue_first2(it);
+
   // ---- Q slices of this wave into registers (B operand: n = query row, k = head dim) ----
   // Row block rb of wave w covers rows m0 + (w*RB + rb)*32 ..; each K or V fragment read
   // from LDS feeds RB MFMAs.  c = softmax_scale * log2(e), the sign included, takes
@@ -248,21 +295,6 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   // tiles below this index need no masking for any row of the workgroup
   const int nfull = CAUSAL ? min(nk / BN, (m0 + 1) / BN) : nk / BN;
 
-  // ---- per-lane addressing of the swizzled tiles ----
-  // Load instruction i of wave ws fills LDS chunks [(i*NW + ws)*64, +64) of the tile;
-  // the per-lane global offsets are relative to the tile's first row, so they do not
-  // depend on the tile.
-  const int ws = __builtin_amdgcn_readfirstlane(w);   // wave index as a scalar
-  int kvo[IPT], vvo[IPT];             // byte offsets from the tile's first row
-#pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const int I = i * NW + ws;
-    const int pch = I * 64 + lane;
-    const int r = pch / CPR;
-    const int cc = TL::logical_chunk(r, pch % CPR);
-    kvo[i] = (int)(r * p.k_ss + cc * 8) * 2;
-    vvo[i] = (int)(r * p.v_ss + cc * 8) * 2;
-  }
   int kaddr[KS];                     // K fragment (row l32, chunk 2t+hh) for 32-key block 0
 #pragma unroll
   for (int t = 0; t < KS; ++t) kaddr[t] = TL::offset(l32, 2 * t + hh);
@@ -483,9 +515,9 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     const int p_hh4 = hh * 4;
     // copy resources of tile jbeg over the rows [jbeg*BN, min(nk, jend*BN)); each copy
     // advances them by one tile, so rows past that range read as zeros
-    // (persistent schedule: with it.pre = 2 the previous item issued the copies of tiles
-    // jbeg and jbeg+1 into slots 0 and 1, and the loop starts copying at jbeg + 2)
-    const int p_npre = __builtin_amdgcn_readfirstlane(it.pre);
+    // (with pre_cur = 2 the copies of tiles jbeg and jbeg+1 into slots 0 and 1 are already
+    // issued, and the loop starts copying at jbeg + 2)
+    const int p_npre = __builtin_amdgcn_readfirstlane(pre_cur);
     const int64_t rows_left = max((int64_t)min(nk, jend * BN) - (int64_t)(jbeg + p_npre) * BN, (int64_t)0);
     const uint64_t ka0 = (uint64_t)(uintptr_t)(kbase + (int64_t)(jbeg + p_npre) * BN * p.k_ss);
     const uint64_t va0 = (uint64_t)(uintptr_t)(vbase + (int64_t)(jbeg + p_npre) * BN * p.v_ss);
@@ -694,34 +726,9 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
 #endif
     }
   }
-  // Persistent schedule: the next item's first two K/V tiles go into slots 0 and 1 (the
-  // copies the loop's prologue would issue) after this item's O stores, so their latency
-  // overlaps those stores and the next item's Q loads.
-  if (PIPE && p.persist && has_next && next.qt * BMW < next.nq) {
-    const int nm0 = next.qt * BMW;
-    const int nkend = CAUSAL ? min(next.nk, nm0 + BMW) : next.nk;
-    const int njend = cdiv(nkend, BN);
-    if (njend >= 2) {
-      const int nhkv = next.hq / (p.Hq / p.Hkv);
-      const T* nkb = (const T*)p.k + (int64_t)next.b * p.k_sb + (int64_t)nhkv * p.k_sh + (int64_t)next.k_off * p.k_ss;
-      const T* nvb = (const T*)p.v + (int64_t)next.b * p.v_sb + (int64_t)nhkv * p.v_sh + (int64_t)next.k_off * p.v_ss;
-      const int64_t nrows = min(next.nk, njend * BN);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int64_t rt = min(max(nrows - (int64_t)t * BN, (int64_t)0), (int64_t)BN);
-        const __amdgpu_buffer_rsrc_t krs = make_rsrc(nkb + (int64_t)t * BN * p.k_ss, (uint32_t)(rt * p.k_ss * 2));
-        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(nvb + (int64_t)t * BN * p.v_ss, (uint32_t)(rt * p.v_ss * 2));
-        T* kdst = smem + t * 2 * PART;
-#pragma unroll
-        for (int i = 0; i < IPT; ++i) {
-          const int I = i * NW + ws;
-          buffer_to_lds16(krs, kvo[i], kdst + I * 64 * 8);
-          buffer_to_lds16(vrs, vvo[i], kdst + PART + I * 64 * 8);
-        }
-      }
-      pre_next = 2;
-    }
-  }
+  // Persistent schedule: the next item's first two K/V tiles are copied after this item's
+  // O stores, so their latency overlaps those stores and the next item's Q loads.
+  if (PIPE && p.persist && has_next) pre_next = issue_first2(next);
 #ifdef FAL_FWD_WGSTAMP
   {
     const uint32_t st2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
