@@ -169,11 +169,14 @@ static int fal_fwd_impl(const void* q, const void* k, const void* v, void* o, fl
     p.gqa4 = 1;
     p.n_qtiles = cdiv((int)seqlen_q, 64);
     nblocks = (int64_t)p.n_qtiles * batch * (heads_q / 4);
-    // at least two items per CU: one persistent workgroup per CU walks pairs of tiles
+  }
+  // pipelined kernel with at least two items per CU: one persistent workgroup per CU
+  // walks pairs of query tiles
+  if (!p.kchunk && fwd_pipe_ok((int)head_dim)) {
     const int ncu = device_cu_count();
     if (FAL_FWD_PERSIST && ncu > 0 && nblocks >= 2 * (int64_t)ncu) {
       p.persist = 1;
-      const int64_t pairs = (int64_t)(p.n_qtiles + 1) / 2 * batch * (heads_q / 4);
+      const int64_t pairs = (int64_t)(p.n_qtiles + 1) / 2 * batch * (heads_q / (p.gqa4 ? 4 : 1));
       nblocks = std::min<int64_t>(pairs, ncu);
     }
   }

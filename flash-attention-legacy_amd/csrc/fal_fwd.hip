@@ -744,9 +744,9 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   return pre_next;
 }
 
-// Persistent schedule (pipelined head_dim-128 kernel under gqa4, batched calls with at
-// least two items per CU): a grid of one workgroup per CU walks pairs of query tiles,
-// (T-1-p, p) under a causal mask so every pair costs the same, (2p, 2p+1) without.  The
+// Persistent schedule (pipelined head_dim-128 kernel, batched calls with at least two
+// items per CU; an item is 64 rows of four heads under gqa4, else 256 rows of one head):
+// a grid of one workgroup per CU walks pairs of query tiles, (T-1-p, p) under a causal mask so every pair costs the same, (2p, 2p+1) without.  The
 // pairs are numbered unit-major (unit = batch, KV head, group of four query heads) and
 // round r gives workgroup w pair r*G + w', w' the XCD-major rank of w, so the
 // workgroups of one XCD work on neighbouring pairs of one unit (shared K/V in that
@@ -758,7 +758,7 @@ __device__ __forceinline__ bool fwd_item_persist(const FwdParams& p, FwdItem& it
   const int wr = (G & 7) == 0 ? (w & 7) * (G >> 3) + (w >> 3) : w;
   const int T = p.n_qtiles;
   const int npair = (T + 1) >> 1;
-  const int g = p.Hq / p.Hkv, ng = g >> 2;
+  const int g = p.Hq / p.Hkv, ng = p.gqa4 ? g >> 2 : g;   // workgroup units per KV head
   // (the host keeps B * Hkv * ng * npair below 2^31)
   const uint32_t e = (uint32_t)(i >> 1) * (uint32_t)G + (uint32_t)wr;
   if (e >= (uint32_t)(p.B * p.Hkv * ng * npair)) return false;
@@ -768,7 +768,8 @@ __device__ __forceinline__ bool fwd_item_persist(const FwdParams& p, FwdItem& it
   if (CAUSAL && half && pp == T - 1 - pp) it.qt = T;   // odd T: the middle tile has no partner
   const int hg = (int)((uint32_t)u % (uint32_t)ng), bh = (int)((uint32_t)u / (uint32_t)ng);
   it.b = (int)((uint32_t)bh / (uint32_t)p.Hkv);
-  it.hq = __builtin_amdgcn_readfirstlane((bh - it.b * p.Hkv) * g + hg * 4 + (int)(threadIdx.x >> 6));
+  it.hq = __builtin_amdgcn_readfirstlane((bh - it.b * p.Hkv) * g +
+                                         (p.gqa4 ? hg * 4 + (int)(threadIdx.x >> 6) : hg));
   it.q_off = 0;
   it.k_off = 0;
   it.nq = p.Nq;
@@ -1108,9 +1109,12 @@ hipError_t launch_fwd_combine(const FwdParams& p, int d, int causal, hipStream_t
 #endif
 // True when a batched (not split) forward of this head dim and head ratio runs the
 // pipelined kernel with the four-heads-per-workgroup layout (FwdParams::gqa4).
+bool fwd_pipe_ok(int d) {
+  return FAL_FWD_PIPE && !FAL_PRESCALE_FP16 && d == 128 && FwdCfg<128>::RB == 2 && FwdCfg<128>::NW == 4 &&
+         FwdCfg<128>::BN == 64;
+}
 bool fwd_gqa4_ok(int d, int64_t heads_q, int64_t heads_kv) {
-  return FAL_FWD_GQA4 && FAL_FWD_PIPE && !FAL_PRESCALE_FP16 && d == 128 && FwdCfg<128>::RB == 2 &&
-         FwdCfg<128>::NW == 4 && FwdCfg<128>::BN == 64 && heads_kv > 0 && (heads_q / heads_kv) % 4 == 0;
+  return FAL_FWD_GQA4 && fwd_pipe_ok(d) && heads_kv > 0 && (heads_q / heads_kv) % 4 == 0;
 }
 
 int fwd_block_m(int d) {

@@ -45,7 +45,7 @@ struct FwdParams {
   // (n_qtiles counts 64-row tiles, the grid B * Hq/4 * n_qtiles), so under a causal mask
   // every wave stops at the same diagonal tile.
   int gqa4;
-  // gqa4 only: persistent grid (one workgroup per CU walking pairs of query tiles)
+  // pipelined kernel: persistent grid (one workgroup per CU walking pairs of query tiles)
   int persist;
 };
 
@@ -115,6 +115,7 @@ struct DecodeParams {
 
 hipError_t launch_fwd(const FwdParams& p, int d, int causal, dim3 grid, hipStream_t st);
 int fwd_block_m(int d);
+bool fwd_pipe_ok(int d);   // batched calls of this head dim run the pipelined tile loop
 bool fwd_gqa4_ok(int d, int64_t heads_q, int64_t heads_kv);   // FwdParams::gqa4 applies
 int fwd_block_m_varlen(int d);   // query rows per workgroup of a packed-sequence call
 int fwd_block_n(int d);

@@ -300,11 +300,13 @@ def _gpu_fp32_attention(q, k, v, scale, causal):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("B,Hq,Hkv,N", [(2, 16, 4, 4160), (1, 32, 4, 4160), (2, 8, 2, 8192)])
+@pytest.mark.parametrize("B,Hq,Hkv,N", [(2, 16, 4, 4160), (1, 32, 4, 4160), (2, 8, 2, 8192),
+                                         (2, 16, 16, 4352), (2, 16, 8, 4352)])
 def test_persistent_grid_every_head(B, Hq, Hkv, N, causal):
-    """head_dim 128 with Hq/Hkv a multiple of 4 and at least two 64-row items per CU runs
-    the persistent grid (pairs of query tiles per workgroup, an odd tile count leaves the
-    middle tile unpaired): every output row of every head against the fp32 formula."""
+    """head_dim 128 with at least two items per CU runs the persistent grid (pairs of query
+    tiles per workgroup; items of 64 rows of four heads when Hq/Hkv is a multiple of 4,
+    else of 256 rows of one head; an odd tile count leaves the middle tile unpaired):
+    every output row of every head against the fp32 formula."""
     d = 128
     scale = 1.0 / math.sqrt(d)
     q, k, v = randn((B, Hq, N, d), seed=21), randn((B, Hkv, N, d), seed=22), randn((B, Hkv, N, d), seed=23)
