@@ -53,7 +53,8 @@ namespace fal {
 // A workgroup's (batch or sequence, query head, query tile) and its row ranges.
 struct FwdItem {
   int b, hq, qt, q_off, k_off, nq, nk, split;
-  int pre;   // persistent schedule: copies of the first two K/V tiles already issued (2) or not (0)
+  int pre;    // persistent schedule: copies of the first two K/V tiles already issued (2) or not (0)
+  int qpre;   // persistent schedule: this item's Q slices already loaded (by the previous item)
 };
 
 // Item `item` of the varlen forward work list for at most 64 sequences, derived in the
@@ -91,6 +92,7 @@ __device__ __forceinline__ bool varlen_item_small(const int* cu, int num_seqs, i
 template <bool CAUSAL>
 __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm) {
   it.pre = 0;
+  it.qpre = 0;
   if (p.cu_q) {
     // 1-D grid over (work item, KV head) groups of G query heads.  Block i runs on XCD
     // i % 8 as that XCD's (i / 8)-th block; the groups are dealt to the XCDs round-robin
@@ -151,11 +153,12 @@ constexpr int kPipeOWave = 32 * kPipeOStr;
 
 // One work item (query tile of one head, or of four heads under gqa4) of fwd_kernel.
 // Every wave of the workgroup takes the same early returns.
-// Returns 2 when it issued the copies of the next item's first two K/V tiles (persistent
-// schedule; `next` is valid when has_next), else 0.
+// Persistent schedule (`next` valid when has_next): returns pre | (qpre << 2) for the next
+// item -- pre = 2 when this item issued the copies of its first two K/V tiles, qpre = 1
+// when it loaded its Q slices into qio (the Q registers, free once the tile loop is done).
 template <class T, int D, int NW, int BN, bool CAUSAL, int RB>
 __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T* smem, const FwdItem& next,
-                                        bool has_next) {
+                                        bool has_next, vec8<T> (&qio)[RB][D / 16]) {
   using TL = SwizzledTile<D>;
   using V8 = vec8<T>;
   using V4 = vec4<T>;
@@ -186,7 +189,7 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   const int w = tid >> 6;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  int pre_next = 0;
+  int pre_next = 0, qpre_next = 0;
   bool stored = false;   // the pipelined path wrote O and L itself
 
   const int b = it.b, hq = it.hq, qt = it.qt, q_off = it.q_off, k_off = it.k_off, nq = it.nq, nk = it.nk;
@@ -265,10 +268,11 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   const bool negq = PIPE_SIGN && p.scale_log2 < 0.f;
   const float c = PIPE_SIGN ? fmaxf(fabsf(p.scale_log2), 1e-30f) : p.scale_log2;
   int row[RB];
-  V8 qreg[RB][KS];
+  V8 (&qreg)[RB][KS] = qio;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    row[rb] = m0 + ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;
+  for (int rb = 0; rb < RB; ++rb) row[rb] = m0 + ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;
+#pragma unroll
+  for (int rb = 0; rb < RB && !it.qpre; ++rb) {
 #pragma unroll
     for (int t = 0; t < KS; ++t) {
       V8 x = row[rb] < nq ? ld8(qbase + (int64_t)row[rb] * p.q_ss + t * 16 + hh * 8) : zero8<T>();
@@ -548,6 +552,23 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
 #ifdef FAL_FWD_WGSTAMP
     st1 = (uint32_t)__builtin_amdgcn_s_memrealtime();
 #endif
+    // persistent schedule: the next item's Q slices load while this item's O goes out
+    // (buffer loads: rows past the sequence read as zeros; a negative scale, folded into
+    // Q, keeps the loads at the item's start)
+    if (p.persist && has_next && !negq && next.qt * BMW < next.nq) {
+      const T* nqb = (const T*)p.q + (int64_t)next.b * p.q_sb + (int64_t)next.hq * p.q_sh + (int64_t)next.q_off * p.q_ss;
+      const __amdgpu_buffer_rsrc_t qrs =
+          make_rsrc(nqb, (uint32_t)min((int64_t)next.nq * p.q_ss * 2, (int64_t)0x7fffffff));
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int nrow = next.qt * BMW + ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;
+        const int qoff = (int)((int64_t)nrow * p.q_ss * 2) + hh * 16;
+#pragma unroll
+        for (int t = 0; t < KS; ++t)
+          qio[rb][t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(qrs, qoff + t * 32, 0, 0));
+      }
+      qpre_next = 1;
+    }
     // O^T accumulator block g (= (rb*DB + db)*4 + g4) of lane l is at byte
     // ws*kPipeOWave + l*16 + g*kPipeOStr: 16 bytes of a row (MFMA layout)
     const char* wbase = (const char*)smem + ws * kPipeOWave;
@@ -586,23 +607,24 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
       }
       const int cch = lane & 15;               // 16-byte chunk of the row
       const int wr0 = m0 + (gqa4 ? 0 : w) * RB * 32;
-      // per row block: all LDS reads and row factors first, then the stores (one wait,
-      // not one per row)
+      // per 16 rows: all LDS reads and row factors first, then the stores (one wait, not
+      // one per row)
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        f32x4 a0[8], a1[8];
-        float iv[8];
+      for (int hb = 0; hb < 2 * RB; ++hb) {
+        const int rb = hb >> 1;
+        f32x4 a0[4], a1[4];
+        float iv[4];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int l32w = jj * 4 + (lane >> 4);
+        for (int jj = 0; jj < 4; ++jj) {
+          const int l32w = (hb & 1) * 16 + jj * 4 + (lane >> 4);
           const int g = rb * 16 + cch;
           a0[jj] = *reinterpret_cast<const f32x4*>(wbase + l32w * 16 + g * kPipeOStr);
           a1[jj] = *reinterpret_cast<const f32x4*>(wbase + (32 + l32w) * 16 + g * kPipeOStr);
           iv[jj] = __shfl(inv[rb], l32w);
         }
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int r = rb * 32 + jj * 4 + (lane >> 4);   // row of the wave, 0..63
+        for (int jj = 0; jj < 4; ++jj) {
+          const int r = hb * 16 + jj * 4 + (lane >> 4);   // row of the wave, 0..63
           V8 h;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -741,7 +763,7 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     }
   }
 #endif
-  return pre_next;
+  return pre_next | (qpre_next << 2);
 }
 
 // Persistent schedule (pipelined head_dim-128 kernel, batched calls with at least two
@@ -776,6 +798,7 @@ __device__ __forceinline__ bool fwd_item_persist(const FwdParams& p, FwdItem& it
   it.nk = p.Nk;
   it.split = 0;
   it.pre = 0;
+  it.qpre = 0;
   return true;
 }
 
@@ -794,10 +817,13 @@ fwd_kernel(FwdParams p) {
     // items past the tile count (qt >= n_qtiles) are skipped inside fwd_body; each item
     // ends with a barrier after its O left LDS and may issue the next item's first copies
     FwdItem nx;
+    vec8<T> qio[RB][D / 16];
     bool have = fwd_item_persist<CAUSAL>(p, it, 0);
     for (int i = 0; have; ++i) {
       const bool more = fwd_item_persist<CAUSAL>(p, nx, i + 1);
-      nx.pre = fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, nx, more);
+      const int r = fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, nx, more, qio);
+      nx.pre = r & 3;
+      nx.qpre = r >> 2;
       it = nx;
       have = more;
     }
@@ -805,7 +831,8 @@ fwd_kernel(FwdParams p) {
   }
   // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
   if (!fwd_item<CAUSAL>(p, it, NW * 32 * RB)) return;
-  fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, it, false);
+  vec8<T> qio[RB][D / 16];
+  fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, it, false, qio);
 }
 
 // ---------------------------------------------------------------------------
