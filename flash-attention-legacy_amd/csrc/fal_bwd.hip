@@ -903,23 +903,37 @@ bwd_kv_pipe_kernel(BwdParams p) {
   const int p_nq = nq, p_nqt = nqt;
   const int64_t qstep = (int64_t)kPipeBM * p.q_ss * 2, dstep = (int64_t)kPipeBM * p.do_ss * 2;
 
+  // K and V of this wave's 32 keys of key tile kt (B operands), buffer loads: keys past
+  // the end read as zeros.  The second tile's are loaded right after the first tile's
+  // loop, so their latency overlaps that tile's epilogue.
+  V8 kreg[8], vreg[8];
+  auto load_kv = [&](int kt) {
+    // one resource per key tile: its rows inside the sequence, offsets from its first row
+    const int n0 = kt * kPipeBN;
+    const int64_t rows = min(max((int64_t)p.Nk - n0, (int64_t)0), (int64_t)kPipeBN);
+    const __amdgpu_buffer_rsrc_t krs =
+        make_rsrc((const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh + (int64_t)n0 * p.k_ss,
+                  (uint32_t)(rows * p.k_ss * 2));
+    const __amdgpu_buffer_rsrc_t vrs =
+        make_rsrc((const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh + (int64_t)n0 * p.v_ss,
+                  (uint32_t)(rows * p.v_ss * 2));
+    const int r = ws * 32 + l32;
+    const int ko = (int)(r * p.k_ss * 2) + hh * 16, vo = (int)(r * p.v_ss * 2) + hh * 16;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      kreg[t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(krs, ko + t * 32, 0, 0));
+      vreg[t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(vrs, vo + t * 32, 0, 0));
+    }
+  };
+  load_kv(kit);
   for (int tile_i = 0; tile_i < 2; ++tile_i) {
     const int kt = tile_i == 0 ? kit : kt_b;
     if (kt < 0) break;
     const int n0 = kt * kPipeBN;
     const int kw0 = n0 + ws * 32;
-    const int key = kw0 + l32;
     const int qt0 = CAUSAL ? n0 / kPipeBM : 0;
     const int ntq = max(nqt - qt0, 0);
     const int nitems = G * ntq;
-    const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)hkv * p.k_sh;
-    const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)hkv * p.v_sh;
-    V8 kreg[8], vreg[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      kreg[t] = key < nk ? ld8(kbase + (int64_t)key * p.k_ss + t * 16 + hh * 8) : zero8<T>();
-      vreg[t] = key < nk ? ld8(vbase + (int64_t)key * p.v_ss + t * 16 + hh * 8) : zero8<T>();
-    }
     __syncthreads();   // the previous tile's epilogue readers are done with the LDS
     if (nitems > 0) {
       const int hq0 = hkv * G;
@@ -945,6 +959,7 @@ bwd_kv_pipe_kernel(BwdParams p) {
       else
         asm volatile(FAL_BWDP_ASM_BF16 : FAL_BWDP_OUTS : FAL_BWDP_INS : FAL_BWDP_CLOBBERS);
     }
+    if (tile_i == 0 && kt_b >= 0) load_kv(kt_b);
     // dV then dK*scale of this wave's keys: piece pc = db*4 + g4 of lane (hh, l32) holds
     // columns 8*pc + hh*4 .. +3 of key kw0 + l32, at which*kKvOPart + pc*kKvOStr + lane*8.
     // Written back row-wise: each 16-byte store instruction covers 4 whole 256-byte rows.
