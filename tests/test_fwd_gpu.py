@@ -299,6 +299,21 @@ def _gpu_fp32_attention(q, k, v, scale, causal):
     return torch.matmul(torch.softmax(s, dim=-1), v.float())
 
 
+def test_persistent_grid_negative_scale():
+    """A negative softmax scale on the persistent grid: the sign is folded into Q, so the
+    next item's Q slices are not loaded early; every head against the fp32 formula."""
+    B, Hq, Hkv, N, d = 2, 16, 4, 4160, 128
+    scale = -1.0 / math.sqrt(d)
+    q, k, v = randn((B, Hq, N, d), seed=24), randn((B, Hkv, N, d), seed=25), randn((B, Hkv, N, d), seed=26)
+    o, _ = ext().forward(q, k, v, scale, True)
+    G = Hq // Hkv
+    for b in range(B):
+        for g in range(Hkv):
+            hs = slice(g * G, (g + 1) * G)
+            ref = _gpu_fp32_attention(q[b:b + 1, hs], k[b:b + 1, g:g + 1], v[b:b + 1, g:g + 1], scale, True)
+            assert float((o[b:b + 1, hs].float() - ref).abs().max()) <= FWD_ATOL, (b, g)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("B,Hq,Hkv,N", [(2, 16, 4, 4160), (1, 32, 4, 4160), (2, 8, 2, 8192),
                                          (2, 16, 16, 4352), (2, 16, 8, 4352)])
