@@ -556,13 +556,16 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     // (buffer loads: rows past the sequence read as zeros; a negative scale, folded into
     // Q, keeps the loads at the item's start)
     if (p.persist && has_next && !negq && next.qt * BMW < next.nq) {
-      const T* nqb = (const T*)p.q + (int64_t)next.b * p.q_sb + (int64_t)next.hq * p.q_sh + (int64_t)next.q_off * p.q_ss;
+      // one resource over the item's rows (offsets from its first row stay small)
+      const int nm0 = next.qt * BMW;
+      const T* nqb = (const T*)p.q + (int64_t)next.b * p.q_sb + (int64_t)next.hq * p.q_sh +
+                     (int64_t)(next.q_off + nm0) * p.q_ss;
       const __amdgpu_buffer_rsrc_t qrs =
-          make_rsrc(nqb, (uint32_t)min((int64_t)next.nq * p.q_ss * 2, (int64_t)0x7fffffff));
+          make_rsrc(nqb, (uint32_t)((int64_t)min(next.nq - nm0, BMW) * p.q_ss * 2));
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const int nrow = next.qt * BMW + ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;
-        const int qoff = (int)((int64_t)nrow * p.q_ss * 2) + hh * 16;
+        const int nrow = ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;   // row within the item
+        const int qoff = nrow * (int)p.q_ss * 2 + hh * 16;
 #pragma unroll
         for (int t = 0; t < KS; ++t)
           qio[rb][t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(qrs, qoff + t * 32, 0, 0));
