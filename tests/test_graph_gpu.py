@@ -77,3 +77,16 @@ def test_graph_varlen_and_decode():
     kc, vc = randn((4, 3000, 4, 128), seed=9), randn((4, 3000, 4, 128), seed=10)
     od, ld = hip_ext.decode(qd, kc, vc, seq, 0.088, return_lse=True)
     replay_check(lambda: tuple(hip_ext.decode(qd, kc, vc, seq, 0.088, return_lse=True)), (od, ld))
+
+
+@pytest.mark.parametrize("hkv", [8, 32])
+def test_graph_persistent_forward(hkv):
+    """Batched head-dim-128 forward on the persistent grid (four heads per workgroup for
+    32/8, 256-row items for MHA), captured and replayed."""
+    from flash_attn_legacy import hip_ext
+    B, Hq, N, d = 2, 32, 2048, 128
+    q = randn((B, Hq, N, d), seed=11)
+    k, v = randn((B, hkv, N, d), seed=12), randn((B, hkv, N, d), seed=13)
+    scale = 1.0 / math.sqrt(d)
+    o, lse = hip_ext.forward(q, k, v, scale, True)
+    replay_check(lambda: hip_ext.forward(q, k, v, scale, True), (o, lse))
