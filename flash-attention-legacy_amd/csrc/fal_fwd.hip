@@ -759,10 +759,15 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     const uint32_t st2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
     if (lane == 0 && w == 0) {
       // one record per item: start, tile loop done, O stored (issued), workgroup
-      const int64_t rec = (int64_t)blockIdx.x * 64 + (it.qt & 63);
-      uint32_t* dst = reinterpret_cast<uint32_t*>(p.lse) + (p.persist ? ((int64_t)(b * p.Hkv + hkv) * (p.Hq / p.Hkv / 4) +
-                          (hq % (p.Hq / p.Hkv)) / 4) * p.n_qtiles + qt : rec) * 4;
-      dst[0] = st0; dst[1] = st1; dst[2] = st2; dst[3] = blockIdx.x;
+      // (record index: the item under the persistent four-heads grid, else the workgroup;
+      // records past the L buffer are dropped)
+      const int64_t rec = (p.persist && p.gqa4) ? ((int64_t)(b * p.Hkv + hkv) * (p.Hq / p.Hkv / 4) +
+                                                   (hq % (p.Hq / p.Hkv)) / 4) * p.n_qtiles + qt
+                                                : (int64_t)blockIdx.x;
+      if ((rec + 1) * 4 <= (int64_t)p.B * p.Hq * p.Nq) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(p.lse) + rec * 4;
+        dst[0] = st0; dst[1] = st1; dst[2] = st2; dst[3] = blockIdx.x;
+      }
     }
   }
 #endif
