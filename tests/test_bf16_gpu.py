@@ -275,3 +275,23 @@ def test_hf_bf16_padded_batch():
     real = mask.bool()
     cos = torch.nn.functional.cosine_similarity(a[real].reshape(1, -1), b[real].reshape(1, -1)).item()
     assert torch.isfinite(a[real]).all() and cos > 0.999, cos
+
+
+@pytest.mark.parametrize("hkv", [4, 16])
+def test_persistent_grid_every_head(hkv):
+    """bf16 head_dim 128 on the persistent forward grid (four heads per workgroup for
+    16/4, 256-row items for MHA): every row of every head within one bf16 ulp of the fp32
+    formula (computed on the GPU)."""
+    from flash_attn_legacy import hip_ext
+    B, Hq, N, d = 2, 16, 4352, 128
+    q, k, v = rbf((B, Hq, N, d), 41), rbf((B, hkv, N, d), 42), rbf((B, hkv, N, d), 43)
+    scale = 1.0 / math.sqrt(d)
+    o, _ = hip_ext.forward(q, k, v, scale, True)
+    G = Hq // hkv
+    mask = torch.triu(torch.ones(N, N, dtype=torch.bool, device="cuda"), 1)
+    for b in range(B):
+        for g in range(hkv):
+            qs = q[b, g * G:(g + 1) * G].float()
+            s = torch.matmul(qs, k[b, g].float().t()) * scale
+            ref = torch.matmul(torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1), v[b, g].float())
+            check_out(o[b, g * G:(g + 1) * G], ref.cpu())
