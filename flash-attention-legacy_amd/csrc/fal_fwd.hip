@@ -196,12 +196,6 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
   const int hkv = hq / (p.Hq / p.Hkv);
   // gqa4 (pipelined loop only): the waves share 64 query rows of different heads
   const bool gqa4 = PIPE && p.gqa4;
-#ifdef FAL_FWD_WGSTAMP
-  // measurement build (wrong results): s_memrealtime stamps per work item (start, tile loop
-  // done, epilogue and next-item copies issued) written over the L buffer
-  const uint32_t st0 = (uint32_t)__builtin_amdgcn_s_memrealtime();
-  uint32_t st1 = 0;
-#endif
   const int BMW = gqa4 ? 32 * RB : BM;      // query rows per workgroup and head
   const int m0 = qt * BMW;
   if (m0 >= nq) return 0;
@@ -542,16 +536,10 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     const int p_jl = __builtin_amdgcn_readfirstlane(jl);
     const int p_jbeg = jbeg, p_jend = jend, p_nk = nk;
     const int p_wrow = CAUSAL ? wrow0 : 0x3fffffff;
-#ifdef FAL_PIPE_DEBUG_CYC
-    uint32_t p_dbg[4];
-#endif
     if constexpr (std::is_same<T, half_t>::value)
       asm volatile(FAL_PIPE_ASM_F16 : FAL_PIPE_OUTS : FAL_PIPE_INS : FAL_PIPE_CLOBBERS);
     else
       asm volatile(FAL_PIPE_ASM_BF16 : FAL_PIPE_OUTS : FAL_PIPE_INS : FAL_PIPE_CLOBBERS);
-#ifdef FAL_FWD_WGSTAMP
-    st1 = (uint32_t)__builtin_amdgcn_s_memrealtime();
-#endif
     // persistent schedule: the next item's Q slices load while this item's O goes out
     // (buffer loads: rows past the sequence read as zeros; a negative scale, folded into
     // Q, keeps the loads at the item's start)
@@ -575,13 +563,6 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
     // O^T accumulator block g (= (rb*DB + db)*4 + g4) of lane l is at byte
     // ws*kPipeOWave + l*16 + g*kPipeOStr: 16 bytes of a row (MFMA layout)
     const char* wbase = (const char*)smem + ws * kPipeOWave;
-#ifdef FAL_PIPE_DEBUG_CYC
-    if (lane == 0 && m0 == 0 && hq == 0 && b == 0) {
-      // debug build: per-wave cycle sums (PV phase, wait + barrier, S phase, iterations)
-      for (int i = 0; i < 4; ++i) obase[ws * 4 + i] = (T)((float)p_dbg[i] / (i < 3 ? 1024.f : 1.f));
-      return 0;
-    }
-#endif
     if (p.kchunk) {
       // split-KV partials: back into the accumulator layout
 #pragma unroll
@@ -603,10 +584,8 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
       for (int rb = 0; rb < RB; ++rb) {
         const float l_tot = pair_sum(l_run[rb]);
         inv[rb] = l_tot > 0.f ? 1.f / l_tot : 0.f;
-#ifndef FAL_FWD_WGSTAMP
         if (hh == 0 && row[rb] < nq)
           lbase[(int64_t)row[rb] * p.l_ss] = l_tot > 0.f ? (m_run[rb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
-#endif
       }
       const int cch = lane & 15;               // 16-byte chunk of the row
       const int wr0 = m0 + (gqa4 ? 0 : w) * RB * 32;
@@ -711,10 +690,8 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
           for (int e = 0; e < 4; ++e) h[e] = (T)(oacc[rb][db][g4 * 4 + e] * inv);
           *reinterpret_cast<V4*>(wst + (rb * 32 + l32) * OROW + (db * 32 + g4 * 8 + hh * 4) * 2) = h;
         }
-#ifndef FAL_FWD_WGSTAMP
       if (hh == 0 && row[rb] < nq)
         lbase[(int64_t)row[rb] * p.l_ss] = l_tot > 0.f ? (m_run[rb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
-#endif
     }
     // (one wave's LDS accesses complete in order: its rows are staged before these reads)
     constexpr int CPRW = D / 8;
@@ -742,35 +719,16 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
           for (int e = 0; e < 4; ++e) h[e] = (T)(oacc[rb][db][g4 * 4 + e] * inv);
           *reinterpret_cast<V4*>(orow + db * 32 + g4 * 8 + hh * 4) = h;
         }
-#ifndef FAL_FWD_WGSTAMP
       if (hh == 0) {
         float L = -INFINITY;
         if (l_tot > 0.f) L = (m_run[rb] + fast_log2(l_tot)) * kLn2;
         lbase[(int64_t)row[rb] * p.l_ss] = L;
       }
-#endif
     }
   }
   // Persistent schedule: the next item's first two K/V tiles are copied after this item's
   // O stores, so their latency overlaps those stores and the next item's Q loads.
   if (PIPE && p.persist && has_next) pre_next = issue_first2(next);
-#ifdef FAL_FWD_WGSTAMP
-  {
-    const uint32_t st2 = (uint32_t)__builtin_amdgcn_s_memrealtime();
-    if (lane == 0 && w == 0) {
-      // one record per item: start, tile loop done, O stored (issued), workgroup
-      // (record index: the item under the persistent four-heads grid, else the workgroup;
-      // records past the L buffer are dropped)
-      const int64_t rec = (p.persist && p.gqa4) ? ((int64_t)(b * p.Hkv + hkv) * (p.Hq / p.Hkv / 4) +
-                                                   (hq % (p.Hq / p.Hkv)) / 4) * p.n_qtiles + qt
-                                                : (int64_t)blockIdx.x;
-      if ((rec + 1) * 4 <= (int64_t)p.B * p.Hq * p.Nq) {
-        uint32_t* dst = reinterpret_cast<uint32_t*>(p.lse) + rec * 4;
-        dst[0] = st0; dst[1] = st1; dst[2] = st2; dst[3] = blockIdx.x;
-      }
-    }
-  }
-#endif
   return pre_next | (qpre_next << 2);
 }
 

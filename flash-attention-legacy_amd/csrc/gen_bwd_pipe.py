@@ -39,7 +39,8 @@ Register plan (per lane; one wave per SIMD: 256 VGPRs and 256 AGPRs):
   s[88:89] compare mask, s90..s93 and s95 temporaries, s94 next item to copy
   v0..v103, a128..a191 and s0..s71 are left to the compiler (K and V arrive in AGPRs).
 
-Run by build.py before compiling; the output is deterministic text.
+The output is deterministic text, tracked under csrc/gen/; build.py checks the tracked
+file against render() and rewrites it only when asked (--regen).
 """
 
 import os
@@ -50,8 +51,16 @@ OSTR = 528              # bytes between the hand-off pieces (kKvOStr in fal_bwd.
 SLOT = 32768
 DOFF = 16384            # dO tile inside a slot
 LDOFF = 131072          # Ls/Dn slots
-ADIST = int(os.environ.get("FAL_BWDP_ADIST", "4"))   # Q/dO fragment reads ahead of their MFMA
-BDIST = int(os.environ.get("FAL_BWDP_BDIST", "6"))   # transposed reads ahead (2 per MFMA)
+# Knobs (set by configure(); the values here are the product kernel's)
+DEFAULTS = {
+    "ADIST": 4,    # Q/dO fragment reads ahead of their MFMA
+    "BDIST": 6,    # transposed reads ahead (2 per MFMA)
+    # measurement builds only (wrong results): comma-separated subset of
+    # nodma, nobar, novalu, nolds, nob (no dV/dK products), noa (no S/dP products)
+    "ABL": "",
+}
+ADIST, BDIST = 4, 6
+DEFAULT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gen", "fal_bwd_pipe.inc")
 
 SET = (128, 192)
 QA = 112
@@ -66,11 +75,7 @@ SM = 88
 ST0, ST1, ST2, ST3, ST4 = 90, 91, 92, 93, 95
 SF = 94
 RSRC_W3 = "0x00020000"
-# Measurement builds only (FAL_BWDP_MEASURE=1; their results are wrong, so a stray
-# variable never reaches a normal build).  FAL_BWDP_ABL: comma-separated subset of
-# nodma, nobar, novalu, nolds, nob (no dV/dK products), noa (no S/dP products)
-MEASURE = os.environ.get("FAL_BWDP_MEASURE") == "1"
-ABL = set(x for x in os.environ.get("FAL_BWDP_ABL", "").split(",") if x) if MEASURE else set()
+MEASURE, ABL = False, set()
 
 # ---- operands: (name, constraint, C++ expression) ----
 OUTS = []
@@ -439,7 +444,33 @@ class Emitter:
         return self.lines
 
 
-def render():
+
+def configure(knobs=None, measure=False):
+    """Set the generator's knobs.  `knobs` maps names of DEFAULTS to values; nothing
+    is read from the environment.  Ablations (ABL) give wrong results and are refused
+    unless `measure` is true."""
+    knobs = dict(knobs or {})
+    bad = set(knobs) - set(DEFAULTS)
+    if bad:
+        raise ValueError(f"unknown generator knobs {sorted(bad)}; known: {sorted(DEFAULTS)}")
+    cfg = {**DEFAULTS, **knobs}
+    if cfg.get("ABL") and not measure:
+        raise ValueError("ablation knobs (ABL) give wrong results; they need a measurement build")
+    g = globals()
+    for k in DEFAULTS:
+        g[k] = type(DEFAULTS[k])(cfg[k]) if k != "ABL" else set(x for x in str(cfg[k]).split(",") if x)
+    g["MEASURE"] = bool(measure)
+
+def render(knobs=None, measure=False):
+    """The generated text for the given knobs (defaults: the product kernel)."""
+    configure(knobs, measure)
+    try:
+        return _render()
+    finally:
+        configure()
+
+
+def _render():
     out = ["// Generated by gen_bwd_pipe.py; do not edit.", "#pragma once", ""]
     for bf16, name in ((False, "FAL_BWDP_ASM_F16"), (True, "FAL_BWDP_ASM_BF16")):
         lines = Emitter(bf16).program()
@@ -459,12 +490,10 @@ def render():
 
 
 def main(path=None):
-    path = path or os.path.join(os.path.dirname(os.path.abspath(__file__)), "fal_bwd_pipe.inc")
-    text = render()
-    old = open(path).read() if os.path.exists(path) else None
-    if old != text:
-        with open(path, "w") as f:
-            f.write(text)
+    """Write the default text to `path` (the tracked file when None)."""
+    path = path or DEFAULT_PATH
+    with open(path, "w") as f:
+        f.write(render())
     return path
 
 

@@ -33,7 +33,8 @@ Register plan (per lane; one wave per SIMD):
   s98/s99 temporaries
   v0..v91, a64..a191 and s0..s83 are left to the compiler (Q and dO arrive in AGPRs).
 
-Run by build.py before compiling; the output is deterministic text.
+The output is deterministic text, tracked under csrc/gen/; build.py checks the tracked
+file against render() and rewrites it only when asked (--regen).
 """
 
 import os
@@ -42,8 +43,14 @@ import sys
 NBUF = 4
 OSTR = 1040             # bytes between the hand-off blocks (kDqOStr in fal_bwd.hip)
 VOFF = 16384
-ADIST = int(os.environ.get("FAL_DQP_ADIST", "4"))   # K/V fragment reads ahead of their MFMA
-QDIST = int(os.environ.get("FAL_DQP_QDIST", "6"))   # transposed reads ahead (2 per MFMA)
+# Knobs (set by configure(); the values here are the product kernel's)
+DEFAULTS = {
+    "ADIST": 4,    # K/V fragment reads ahead of their MFMA
+    "QDIST": 6,    # transposed reads ahead (2 per MFMA)
+}
+ADIST, QDIST = 4, 6
+MEASURE = False
+DEFAULT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gen", "fal_dq_pipe.inc")
 
 SET = (128, 192)
 DN = 92             # v[92:107]: -D in every register (the dP^T accumulators' start)
@@ -426,7 +433,33 @@ class Emitter:
         return self.lines
 
 
-def render():
+
+def configure(knobs=None, measure=False):
+    """Set the generator's knobs.  `knobs` maps names of DEFAULTS to values; nothing
+    is read from the environment.  Ablations (ABL) give wrong results and are refused
+    unless `measure` is true."""
+    knobs = dict(knobs or {})
+    bad = set(knobs) - set(DEFAULTS)
+    if bad:
+        raise ValueError(f"unknown generator knobs {sorted(bad)}; known: {sorted(DEFAULTS)}")
+    cfg = {**DEFAULTS, **knobs}
+    if cfg.get("ABL") and not measure:
+        raise ValueError("ablation knobs (ABL) give wrong results; they need a measurement build")
+    g = globals()
+    for k in DEFAULTS:
+        g[k] = type(DEFAULTS[k])(cfg[k]) if k != "ABL" else set(x for x in str(cfg[k]).split(",") if x)
+    g["MEASURE"] = bool(measure)
+
+def render(knobs=None, measure=False):
+    """The generated text for the given knobs (defaults: the product kernel)."""
+    configure(knobs, measure)
+    try:
+        return _render()
+    finally:
+        configure()
+
+
+def _render():
     out = ["// Generated by gen_dq_pipe.py; do not edit.", "#pragma once", ""]
     for bf16, name in ((False, "FAL_DQP_ASM_F16"), (True, "FAL_DQP_ASM_BF16")):
         lines = Emitter(bf16).program()
@@ -446,12 +479,10 @@ def render():
 
 
 def main(path=None):
-    path = path or os.path.join(os.path.dirname(os.path.abspath(__file__)), "fal_dq_pipe.inc")
-    text = render()
-    old = open(path).read() if os.path.exists(path) else None
-    if old != text:
-        with open(path, "w") as f:
-            f.write(text)
+    """Write the default text to `path` (the tracked file when None)."""
+    path = path or DEFAULT_PATH
+    with open(path, "w") as f:
+        f.write(render())
     return path
 
 

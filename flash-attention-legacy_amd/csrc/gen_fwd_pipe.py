@@ -43,7 +43,8 @@ Register plan (per lane; one wave per SIMD: 256 VGPRs and 256 AGPRs):
   s96 tile j, s97 next tile to copy, s98/s99 temporaries
   v0..v103, a128..a207 and s0..s83 are left to the compiler (Q arrives in AGPRs).
 
-Run by build.py before compiling; the output is deterministic text.
+The output is deterministic text, tracked under csrc/gen/; build.py checks the tracked
+file against render() and rewrites it only when asked (--regen).
 """
 
 import os
@@ -52,11 +53,20 @@ import sys
 NBUF = 4            # LDS ring slots
 OSTR = 1040         # bytes between a wave's O blocks in the LDS hand-off (kPipeOStr in fal_fwd.hip)
 VOFF = 16384        # V offset inside a slot (bytes)
-KDIST = int(os.environ.get("FAL_PIPE_KDIST", "2"))   # K read-ahead (k-steps of 2 fragments)
-VRING = int(os.environ.get("FAL_PIPE_VRING", "4"))   # V^T fragment ring (pairs of transposed reads)
-VDIST = int(os.environ.get("FAL_PIPE_VDIST", "3"))   # V^T read-ahead (fragment pairs), < VRING
-DMA_AUX = os.environ.get("FAL_PIPE_DMA_AUX", "")       # cache-policy bits of the tile copies
-GSTRIDE = int(os.environ.get("FAL_PIPE_GSTRIDE", "1"))   # MFMAs between two copy instructions
+# Knobs (set by configure(); the values here are the product kernel's)
+DEFAULTS = {
+    "KDIST": 2,       # K read-ahead (k-steps of 2 fragments)
+    "VRING": 4,       # V^T fragment ring (pairs of transposed reads)
+    "VDIST": 3,       # V^T read-ahead (fragment pairs), < VRING
+    "DMA_AUX": "",    # cache-policy bits of the tile copies
+    "GSTRIDE": 1,     # MFMAs between two copy instructions
+    # measurement builds only (wrong results): comma-separated subset of
+    # nodma, nowait, nobar, novalu, nolds, dmasame, dmazero
+    "ABL": "",
+}
+KDIST, VRING, VDIST, DMA_AUX, GSTRIDE = 2, 4, 3, "", 1
+MEASURE, ABL = False, set()
+DEFAULT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gen", "fal_fwd_pipe.inc")
 
 SA = (128, 192)
 VF = 256 - 4 * VRING   # AGPR: V^T ring at the top, K ring below it
@@ -70,11 +80,6 @@ SM, SM0, SR = 84, 86, 87
 SK, SV = 88, 92
 SJ, SD, ST, ST2 = 96, 97, 98, 99
 NEG_INF = "0xff800000"
-# Measurement builds only (FAL_PIPE_MEASURE=1; their results are wrong, so a stray
-# variable never reaches a normal build).  FAL_PIPE_ABL: comma-separated subset of
-# nodma, nowait, nobar, novalu, nolds
-MEASURE = os.environ.get("FAL_PIPE_MEASURE") == "1"
-ABL = set(x for x in os.environ.get("FAL_PIPE_ABL", "").split(",") if x) if MEASURE else set()
 
 # ---- operands: (name, constraint, C++ expression) ----
 OUTS = [("m0", "+v", "m_run[0]"), ("m1", "+v", "m_run[1]"), ("l0", "+v", "l_run[0]"), ("l1", "+v", "l_run[1]")]
@@ -100,12 +105,6 @@ INS += [("c", "s", "c"), ("jbeg", "s", "p_jbeg"), ("jend", "s", "p_jend"), ("jl"
         ("wrow", "s", "p_wrow"), ("nk", "s", "p_nk"), ("ktb", "s", "p_ktb"), ("vtb", "s", "p_vtb"),
         ("krb", "s", "p_krb"), ("vrb", "s", "p_vrb"), ("rows", "s", "p_rows"),
         ("lbase", "s", "p_lbase"), ("npre", "s", "p_npre")]
-# FAL_PIPE_DEBUG=CYC: per-wave cycle sums of the iteration phases; =S: raw scores of the
-# first tile instead of O
-DEBUG = os.environ.get("FAL_PIPE_DEBUG") if MEASURE else None
-DBG_CYC = DEBUG == "CYC"
-if DBG_CYC:
-    OUTS += [(f"dbg{i}", "=s", f"p_dbg[{i}]") for i in range(4)]
 IDX = {name: i for i, (name, _, _) in enumerate(OUTS + INS)}
 
 
@@ -409,16 +408,6 @@ class Emitter:
         e(f"s_or_b64 vcc, vcc, s[{SM}:{SM + 1}]")
         e(f"s_cbranch_vccnz {lbl_fix}")
 
-    def stamp(self, acc):
-        """debug: s[acc] += now - s76, s76 = now"""
-        if not DBG_CYC:
-            return
-        self.e("s_memtime s[80:81]")
-        self.e("s_waitcnt lgkmcnt(0)")
-        self.e(f"s_sub_u32 s77, s80, s76")
-        self.e(f"s_add_u32 s{acc}, s{acc}, s77")
-        self.e("s_mov_b32 s76, s80")
-
     def soft_iteration(self, par, pv, snext, L):
         """Iteration j with the softmax of tile j (scores in SA[par])."""
         e = self.e
@@ -435,23 +424,16 @@ class Emitter:
         else:
             self.dma()
             self.es(soft0)
-        if pv and snext:
-            self.stamp(78)
         if "nowait" not in ABL:
             e("s_waitcnt vmcnt(8)")
         if "nobar" not in ABL:
             e("s_barrier")
-        if pv and snext:
-            self.stamp(79)
         soft1 = self.softmax_ops(par, 1)
         if snext:
             reads, mf = self.s_prod(par ^ 1)
             self.interleave(reads, mf, 2 * KDIST, soft1)
         else:
             self.es(soft1)
-        if pv and snext and DBG_CYC:
-            self.stamp(82)
-            e("s_add_u32 s83, s83, 1")
         if not ABL:
             self.fix_check(L(f"fix{par}", shared=True))
         e(f"s_branch {L(f'cont{par}', shared=True)}")
@@ -501,29 +483,12 @@ class Emitter:
         e(f"s_cbranch_scc1 {L('disp', shared=True)}")
         self.es(self.slot(f"s{ST}", 0))
         self.s_simple(0)
-        if DEBUG == "S":
-            # debug: raw S^T of the first tile to the O hand-off area, l = 1/2 per lane
-            e("s_nop 15")
-            for g in range(16):
-                e(f"ds_write_b128 {op('olds')}, {vr(SA[0] + 4 * g, 4)} offset:{g * OSTR}")
-            e("s_waitcnt lgkmcnt(0)")
-            e(f"v_mov_b32 {op('l0')}, 0.5")
-            e(f"v_mov_b32 {op('l1')}, 0.5")
-            e(f"s_mov_b32 m0, s{SM0}")
-            e(f"s_branch {L('dbgout', shared=True)}")
         self.mask_block(0, L("pmask"))
         e("s_nop 4")
         self.init_max(L("noinit"))
 
         # ---- per-iteration dispatch (uniform per wave) ----
-        if DBG_CYC:
-            for r in (78, 79, 82, 83):
-                e(f"s_mov_b32 s{r}, 0")
         e(f"{L('disp', shared=True)}:")
-        if DBG_CYC:
-            e("s_memtime s[80:81]")
-            e("s_waitcnt lgkmcnt(0)")
-            e("s_mov_b32 s76, s80")
         e(f"s_sub_u32 s{ST}, s{SJ}, {op('jbeg')}")
         e(f"s_and_b32 s{ST}, s{ST}, 1")
         e(f"s_cmp_eq_u32 s{ST}, 0")
@@ -605,15 +570,38 @@ class Emitter:
             e(f"ds_write_b128 {op('olds')}, {ar(4 * g, 4)} offset:{g * OSTR}")
         e("s_waitcnt lgkmcnt(0)")
         e(f"s_mov_b32 m0, s{SM0}")
-        if DBG_CYC:
-            for i, r in enumerate((78, 79, 82, 83)):
-                e(f"s_mov_b32 {op(f'dbg{i}')}, s{r}")
-        if DEBUG == "S":
-            e(f"{L('dbgout', shared=True)}:")
         return self.lines
 
 
-def render():
+
+def configure(knobs=None, measure=False):
+    """Set the generator's knobs.  `knobs` maps names of DEFAULTS to values; nothing
+    is read from the environment.  Ablations (ABL) give wrong results and are refused
+    unless `measure` is true."""
+    knobs = dict(knobs or {})
+    bad = set(knobs) - set(DEFAULTS)
+    if bad:
+        raise ValueError(f"unknown generator knobs {sorted(bad)}; known: {sorted(DEFAULTS)}")
+    cfg = {**DEFAULTS, **knobs}
+    if cfg["ABL"] and not measure:
+        raise ValueError("ablation knobs (ABL) give wrong results; they need a measurement build")
+    g = globals()
+    for k in DEFAULTS:
+        g[k] = type(DEFAULTS[k])(cfg[k]) if k != "ABL" else set(x for x in str(cfg[k]).split(",") if x)
+    g["MEASURE"] = bool(measure)
+    g["VF"] = 256 - 4 * g["VRING"]
+    g["KF"] = g["VF"] - 32
+
+def render(knobs=None, measure=False):
+    """The generated text for the given knobs (defaults: the product kernel)."""
+    configure(knobs, measure)
+    try:
+        return _render()
+    finally:
+        configure()
+
+
+def _render():
     out = ["// Generated by gen_fwd_pipe.py; do not edit.", "#pragma once", ""]
     for bf16, name in ((False, "FAL_PIPE_ASM_F16"), (True, "FAL_PIPE_ASM_BF16")):
         lines = Emitter(bf16).program()
@@ -624,24 +612,20 @@ def render():
     outs = ", ".join(f'"{c}"({x})' for _, c, x in OUTS)
     ins = ", ".join(f'"{c}"({x})' for _, c, x in INS)
     clob = ", ".join([f'"v{i}"' for i in range(104, 256)] + [f'"a{i}"' for i in range(0, 128)] +
-                     [f'"a{i}"' for i in range(KF, 256)] + [f'"s{i}"' for i in range(76 if DBG_CYC else 84, 100)] +
+                     [f'"a{i}"' for i in range(KF, 256)] + [f'"s{i}"' for i in range(84, 100)] +
                      ['"vcc"', '"scc"', '"memory"'])
     out.append(f"#define FAL_PIPE_OUTS {outs}")
     out.append(f"#define FAL_PIPE_INS {ins}")
     out.append(f"#define FAL_PIPE_CLOBBERS {clob}")
-    if DBG_CYC:
-        out.append("#define FAL_PIPE_DEBUG_CYC 1")
     out.append("")
     return "\n".join(out)
 
 
 def main(path=None):
-    path = path or os.path.join(os.path.dirname(os.path.abspath(__file__)), "fal_fwd_pipe.inc")
-    text = render()
-    old = open(path).read() if os.path.exists(path) else None
-    if old != text:
-        with open(path, "w") as f:
-            f.write(text)
+    """Write the default text to `path` (the tracked file when None)."""
+    path = path or DEFAULT_PATH
+    with open(path, "w") as f:
+        f.write(render())
     return path
 
 
