@@ -18,7 +18,8 @@ one JSON object:
   GPU holds under sustained load rather than in the ramp after the host-side input
   creation left it idle;
 * ``cpu_baseline``: fp32 PyTorch attention (the reference's own test formula) on
-  this host's CPU cores over a bounded sample of the same workload;
+  this host's CPU cores over the whole C2 workload (its 32 (batch, KV-group) slices,
+  the GPU call's seeded inputs), median of 3 passes;
 * ``extra``: the other configurations measured the same way -- C1 forward, C3
   backward (2.5x forward flops), C4 varlen forward, C5 split-K decode (KV bytes
   read, GB/s against 8 TB/s HBM), and the reference's packed-vs-padded varlen
@@ -31,6 +32,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -46,8 +48,10 @@ METRIC = "attn fwd/bwd TFLOP/s (% fp16 MFMA peak); decode KV GB/s (% HBM peak)"
 
 
 def randn(shape, seed, device="cuda"):
+    """fp16 N(0,1) drawn on the CPU from a seeded generator; `device` None keeps it there."""
     g = torch.Generator().manual_seed(seed)
-    return torch.randn(shape, generator=g, dtype=torch.float32).half().to(device)
+    x = torch.randn(shape, generator=g, dtype=torch.float32).half()
+    return x.to(device) if device is not None else x
 
 
 def fwd_flops(b, hq, nq, nk, d, causal):
@@ -237,29 +241,34 @@ def bench_varlen_vs_padded(steps, warmup):
     return out
 
 
-def cpu_baseline(budget_s=15.0):
-    """fp32 PyTorch attention (reference tests/test_flash_attn.py:19-32) on the host CPU,
-    over (batch, KV-group) slices of C2 -- 4 query heads x N=4096 x d=128, causal --
-    until `budget_s` seconds have been spent.  Rate in TFLOP/s (same flop convention)."""
+def cpu_baseline(runs=3, budget_s=60.0):
+    """fp32 PyTorch attention (reference tests/test_flash_attn.py:19-32) on the host CPU
+    over the whole C2 workload, on the same seeded inputs as the GPU call: every one of
+    the 32 (batch, KV-group) slices (4 query heads x N=4096 x d=128, causal; one slice at
+    a time bounds the fp32 score matrix), `runs` passes, median pass time (one pass when
+    a pass takes longer than `budget_s` / runs).  Rate in TFLOP/s (same flop convention)."""
     from oracle.torch_ref import ref_attention
     # the GPU box grants one GPU's job 16 CPUs, whatever os.cpu_count() reports
     threads = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(threads)
     B, Hq, Hkv, N, d = 4, 32, 8, 4096, 128
-    gen = torch.Generator().manual_seed(0)
-    q = torch.randn((1, 4, N, d), generator=gen).half()
-    k = torch.randn((1, 1, N, d), generator=gen).half()
-    v = torch.randn((1, 1, N, d), generator=gen).half()
+    G = Hq // Hkv
+    q, k, v = (randn(s, seed, device=None) for s, seed in (((B, Hq, N, d), 0), ((B, Hkv, N, d), 1),
+                                                            ((B, Hkv, N, d), 2)))
     scale = 1.0 / math.sqrt(d)
-    ref_attention(q[:, :, :256], k[:, :, :256], v[:, :, :256], scale, True)   # warm the thread pool
-    done, t0 = 0, time.perf_counter()
-    while True:
-        ref_attention(q, k, v, scale, True)
-        done += 1
-        if time.perf_counter() - t0 >= budget_s or done >= B * Hkv:
+    ref_attention(q[:1, :G, :256], k[:1, :1, :256], v[:1, :1, :256], scale, True)   # warm the thread pool
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for b in range(B):
+            for g in range(Hkv):
+                ref_attention(q[b:b + 1, g * G:(g + 1) * G], k[b:b + 1, g:g + 1], v[b:b + 1, g:g + 1],
+                              scale, True)
+        times.append(time.perf_counter() - t0)
+        if sum(times) * runs > budget_s:
             break
-    dt = time.perf_counter() - t0
-    flops = done * fwd_flops(1, 4, N, N, d, True)
+    dt = statistics.median(times)
+    flops = fwd_flops(B, Hq, N, N, d, True)
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -271,8 +280,10 @@ def cpu_baseline(budget_s=15.0):
         pass
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{done} of the 32 (batch, KV-group) slices of C2 (4 query heads x N=4096 x d=128, "
-                      f"causal), fp32 torch on CPU, {dt:.1f} s; threads={threads}, os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
+            "sample": f"all 32 (batch, KV-group) slices of C2 (4 query heads x N=4096 x d=128, causal each), "
+                      f"the GPU call's seeded inputs, fp32 torch on CPU; median of {len(times)} passes "
+                      f"({', '.join(f'{t:.2f}' for t in times)} s); threads={threads}, "
+                      f"os.cpu_count()={os.cpu_count()}; cpu={cpu_model}"}
 
 
 def load_traffic():

@@ -4,6 +4,7 @@
 // it validates shapes, strides and alignment, lays out the caller-provided
 // workspace, fills the kernel parameter blocks and enqueues the kernels on the
 // caller's stream.  It never allocates device memory and never synchronises.
+#include <atomic>
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
@@ -108,14 +109,19 @@ size_t fal_fwd_workspace_size(int64_t batch, int64_t heads_q, int64_t seqlen_q, 
 #define FAL_FWD_PERSIST 1
 #endif
 // Compute units of the current device (cached per device; 0 if the query fails).
+// Entries are atomics: concurrent first calls on one device may both query it and store
+// the same value.
 static int device_cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev < 64) cached[dev] = n;
+  if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 

@@ -238,8 +238,12 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int64_t rt = min(max(xrows - (int64_t)t * BN, (int64_t)0), (int64_t)BN);
-      const __amdgpu_buffer_rsrc_t krs = make_rsrc(xkb + (int64_t)t * BN * p.k_ss, (uint32_t)(rt * p.k_ss * 2));
-      const __amdgpu_buffer_rsrc_t vrs = make_rsrc(xvb + (int64_t)t * BN * p.v_ss, (uint32_t)(rt * p.v_ss * 2));
+      // record counts clamped as in load_tile (rt <= BN rows: below 2^31 under the host's
+      // sequence-stride limit anyway)
+      const __amdgpu_buffer_rsrc_t krs =
+          make_rsrc(xkb + (int64_t)t * BN * p.k_ss, (uint32_t)min(rt * p.k_ss * 2, (int64_t)0x7fffffff));
+      const __amdgpu_buffer_rsrc_t vrs =
+          make_rsrc(xvb + (int64_t)t * BN * p.v_ss, (uint32_t)min(rt * p.v_ss * 2, (int64_t)0x7fffffff));
       T* kdst = smem + t * 2 * PART;
 #pragma unroll
       for (int i = 0; i < IPT; ++i) {
@@ -548,12 +552,14 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
       const int nm0 = next.qt * BMW;
       const T* nqb = (const T*)p.q + (int64_t)next.b * p.q_sb + (int64_t)next.hq * p.q_sh +
                      (int64_t)(next.q_off + nm0) * p.q_ss;
+      // (at most 256 rows of a sequence stride below 2^22 elements: the byte counts and
+      // offsets below are under 2^31; computed in 64 bits and clamped all the same)
       const __amdgpu_buffer_rsrc_t qrs =
-          make_rsrc(nqb, (uint32_t)((int64_t)min(next.nq - nm0, BMW) * p.q_ss * 2));
+          make_rsrc(nqb, (uint32_t)min((int64_t)min(next.nq - nm0, BMW) * p.q_ss * 2, (int64_t)0x7fffffff));
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const int nrow = ((gqa4 ? 0 : w) * RB + rb) * 32 + l32;   // row within the item
-        const int qoff = nrow * (int)p.q_ss * 2 + hh * 16;
+        const int qoff = (int)min((int64_t)nrow * p.q_ss * 2 + hh * 16, (int64_t)0x7fffffff);
 #pragma unroll
         for (int t = 0; t < KS; ++t)
           qio[rb][t] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(qrs, qoff + t * 32, 0, 0));

@@ -28,6 +28,24 @@ def ref_attention(q, k, v, scale, is_causal=False):
     return torch.matmul(p, v.float())
 
 
+def ref_attention_lse(q, k, v, scale, is_causal=False):
+    """:func:`ref_attention` plus the per-row log-sum-exp in natural log,
+    ``L = m + ln(max(l, 1e-20))`` (``flash_attn_fwd_volta.cu:343``), -inf for rows with
+    no key.  Returns fp32 (O, L)."""
+    h_q, h_kv = q.shape[1], k.shape[1]
+    if h_kv < h_q:
+        k = k.repeat_interleave(h_q // h_kv, dim=1)
+        v = v.repeat_interleave(h_q // h_kv, dim=1)
+    s = torch.matmul(q.float(), k.float().transpose(-2, -1)) * scale
+    if is_causal:
+        n_q, n_k = q.shape[-2], k.shape[-2]
+        mask = torch.triu(torch.ones(n_q, n_k, dtype=torch.bool), diagonal=1)
+        s.masked_fill_(mask, float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    p = torch.exp(s - torch.where(torch.isfinite(lse), lse, torch.zeros_like(lse))[..., None])
+    return torch.matmul(p, v.float()), lse
+
+
 def ref_backward(q, k, v, grad_out, scale, is_causal=False):
     """fp32 autograd of :func:`ref_attention`; dK/dV summed over GQA groups
     (``tests/test_flash_attn.py:35-58``).  Returns fp32 gradients."""

@@ -168,28 +168,14 @@ def test_long_sequence_sampled_gradients():
     assert rel_err(dv[0, 0, keys], torch.from_numpy(np.stack(dv_ref))) <= GRAD_RTOL
 
 
-def _gpu_fp32_grads(q, k, v, do, scale, causal):
-    """fp32 autograd of softmax(QK^T*scale + top-left mask)V on the GPU for one KV group
-    (the formula of oracle/torch_ref.py; used where the CPU would take minutes)."""
-    reps = q.shape[1] // k.shape[1]
-    qf = q.float().requires_grad_(True)
-    kf = k.float().requires_grad_(True)
-    vf = v.float().requires_grad_(True)
-    s = torch.matmul(qf, kf.repeat_interleave(reps, dim=1).transpose(-2, -1)) * scale
-    if causal:
-        n_q, n_k = q.shape[-2], k.shape[-2]
-        s = s.masked_fill(torch.triu(torch.ones(n_q, n_k, dtype=torch.bool, device=q.device), 1), float("-inf"))
-    o = torch.matmul(torch.softmax(s, dim=-1), vf.repeat_interleave(reps, dim=1))
-    o.backward(do.float())
-    return qf.grad, kf.grad, vf.grad
-
-
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("B,Hq,Hkv,N", [(2, 16, 16, 4096), (1, 32, 8, 4160)])
 def test_large_grid_every_head(B, Hq, Hkv, N, causal):
     """head_dim 128 backward on grids of several workgroups per CU (pipelined dQ and dK/dV
     kernels; an odd tile count leaves one query tile unpaired): every gradient of every
-    head against fp32 autograd."""
+    head against the CPU oracle's fp32 autograd (tests/test_flash_attn.py:35-58)."""
+    from oracle.torch_ref import ref_backward
+    torch.set_num_threads(max(torch.get_num_threads(), 8))
     d = 128
     scale = 1.0 / math.sqrt(d)
     q, do = randn((B, Hq, N, d), seed=31), randn((B, Hq, N, d), seed=34)
@@ -199,8 +185,21 @@ def test_large_grid_every_head(B, Hq, Hkv, N, causal):
     for b in range(B):
         for g in range(Hkv):
             hs = slice(g * G, (g + 1) * G)
-            ref = _gpu_fp32_grads(q[b:b + 1, hs], k[b:b + 1, g:g + 1], v[b:b + 1, g:g + 1],
-                                  do[b:b + 1, hs], scale, causal)
+            ref = ref_backward(q[b:b + 1, hs].cpu(), k[b:b + 1, g:g + 1].cpu(), v[b:b + 1, g:g + 1].cpu(),
+                               do[b:b + 1, hs].cpu(), scale, causal)
             for name, got, r in zip(("dq", "dk", "dv"), (dq[b:b + 1, hs], dk[b:b + 1, g:g + 1],
                                                            dv[b:b + 1, g:g + 1]), ref):
                 assert rel_err(got, r) <= GRAD_RTOL, (name, b, g)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,Hq,Hkv,N", [(2, 4, 4, 200), (2, 8, 2, 333), (1, 8, 2, 1000)])
+def test_negative_scale_head_dim_128(B, Hq, Hkv, N, causal):
+    """A negative softmax scale through the pipelined head-dim-128 backward (its
+    accumulators start at -L*log2(e)/c with c of either sign, masked scores take the
+    value whose product with c is -inf): MHA and GQA, row counts that are not a
+    multiple of 64, against the float64 oracle."""
+    d = 128
+    q, do = randn((B, Hq, N, d), seed=81), randn((B, Hq, N, d), seed=84)
+    k, v = randn((B, Hkv, N, d), seed=82), randn((B, Hkv, N, d), seed=83)
+    check(q, k, v, do, -1.0 / math.sqrt(d), causal)

@@ -209,6 +209,18 @@ def test_torch_fp32_reference_agrees_with_float64_oracle():
         a = torch_ref.ref_attention(q, k, v, 0.25, causal)
         b, _ = orc.attention_fwd(q.numpy(), k.numpy(), v.numpy(), 0.25, causal)
         np.testing.assert_allclose(a.numpy(), b, atol=1e-5)
+        o2, l2 = torch_ref.ref_attention_lse(q, k, v, 0.25, causal)
+        b2, lb = orc.attention_fwd(q.numpy(), k.numpy(), v.numpy(), 0.25, causal)
+        np.testing.assert_allclose(o2.numpy(), b2, atol=1e-5)
+        np.testing.assert_allclose(l2.numpy(), lb, atol=1e-5)
+    # L is the natural-log logsumexp of the scaled scores; Nq > Nk leaves no causal row
+    # without a key, Nq < Nk under a causal mask checks the top-left alignment
+    q2 = torch.randn(1, 2, 9, 16, generator=torch.Generator().manual_seed(7))
+    _, l3 = torch_ref.ref_attention_lse(q2, k[:, :, :5], v[:, :, :5], 0.25, True)
+    s3 = torch.einsum("hqd,hkd->hqk", q2[0].double(), k[0, :, :5].double().repeat_interleave(1, 0)) * 0.25
+    for r in range(9):
+        ref = torch.logsumexp(s3[:, r, : min(r + 1, 5)], dim=-1)
+        np.testing.assert_allclose(l3[0, :, r].numpy(), ref.numpy(), atol=1e-5)
     do = torch.randn(1, 4, 33, 16, generator=torch.Generator().manual_seed(6))
     ga = torch_ref.ref_backward(q, k, v, do, 0.25, True)
     gb = orc.attention_bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), 0.25, True)

@@ -145,6 +145,36 @@ def test_config_c4_forward():
             assert max_abs(o[c[i]:c[i + 1], hs], ref) <= FWD_ATOL, (i, g)
 
 
+def test_config_c4_backward():
+    """C4 lengths (16 sequences of U[64, 4096] tokens), 32/8 heads, d=128, causal: the
+    native one-launch varlen backward against the per-sequence semantics of the
+    reference's loop (flash_attn_legacy/flash_attn.py:133-157; dK/dV of a sequence come
+    from its own rows only).  dQ, dK and dV of KV groups 0, 3 and 7 of every sequence
+    against the CPU oracle's fp32 autograd, L and O from this library's forward."""
+    from oracle.torch_ref import ref_backward
+    lens = c4_lengths()
+    tot, hq, hkv, d = sum(lens), 32, 8, 128
+    q, k, v, do = (randn((tot, h, d), seed=s) for s, h in ((0, hq), (1, hkv), (2, hkv), (3, hq)))
+    cu = cu_from_lens(lens)
+    scale = 1.0 / math.sqrt(d)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    varlen(qg, kg, vg, cu, cu, max(lens), max(lens), scale, True).backward(do)
+    dq, dk, dv = (t.grad.cpu() for t in (qg, kg, vg))
+    for t in (dq, dk, dv):
+        assert torch.isfinite(t).all()
+    torch.set_num_threads(max(torch.get_num_threads(), 8))
+    c = cu.cpu().tolist()
+    sw = lambda x: x.permute(1, 0, 2)[None].cpu()
+    for i in range(len(lens)):
+        r = slice(c[i], c[i + 1])
+        for g in (0, 3, hkv - 1):
+            hs, gs = slice(g * 4, g * 4 + 4), slice(g, g + 1)
+            ref = ref_backward(sw(q[r, hs]), sw(k[r, gs]), sw(v[r, gs]), sw(do[r, hs]), scale, True)
+            for name, got, rg in zip(("dq", "dk", "dv"), (dq[r, hs], dk[r, gs], dv[r, gs]), ref):
+                e = rel_err(got, rg[0].permute(1, 0, 2))
+                assert e <= GRAD_RTOL, (name, i, g, e)
+
+
 @pytest.mark.parametrize("d", [96, 128])
 def test_malformed_cu_seqlens_are_clamped(d):
     """A cu_seqlens array past the packed tensor (last entry total + 50, a second

@@ -59,12 +59,25 @@ def test_noalloc_matches_workspace_entry_point_twice():
 
 
 def test_noalloc_rejects_oversized_calls():
+    """A call whose workspace would pass the array's 16 MiB fails with FAL_ERR_WORKSPACE.
+    Every pointer is a real device buffer that a launch could use safely (cache lengths 0,
+    zero K/V strides onto one row), so a regression in the order of the checks would
+    show as a failed assertion, not as a launch on invalid addresses."""
     from flash_attn_legacy import hip_ext
     B, Hq, Hkv, S, d = 64, 64, 8, 1 << 17, 128
     need = hip_ext._lib.fal_decode_workspace_size(B, Hq, Hkv, S, d)
     assert need > 16 << 20
-    s3 = (ctypes.c_int64 * 3)(1 << 20, 1 << 12, 0)
-    rc = hip_ext._lib.fal_decode_noalloc(16, 16, 16, 16, None, 0, 16, None, B, Hq, Hkv, d, S,
-                                         s3, s3, s3, s3, ctypes.c_float(0.1), None)
+    q = torch.zeros((B, Hq, d), dtype=torch.float16, device="cuda")
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device="cuda")
+    row = torch.zeros((d,), dtype=torch.float16, device="cuda")     # every K/V address lands here
+    seq = torch.zeros((B,), dtype=torch.int32, device="cuda")
+    qs = (ctypes.c_int64 * 3)(Hq * d, d, 0)
+    kvs = (ctypes.c_int64 * 3)(0, 0, 0)
+    rc = hip_ext._lib.fal_decode_noalloc(q.data_ptr(), row.data_ptr(), row.data_ptr(), seq.data_ptr(), None, 0,
+                                         o.data_ptr(), lse.data_ptr(), B, Hq, Hkv, d, S,
+                                         qs, kvs, kvs, qs, ctypes.c_float(0.1),
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
     assert rc == FAL_ERR_WORKSPACE
     assert "16777216" in hip_ext._lib.fal_last_error().decode()
