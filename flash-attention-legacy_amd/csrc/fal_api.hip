@@ -211,11 +211,15 @@ int fal_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* ls
                       stream, 1);
 }
 
+#ifndef FAL_FWD_VARLEN_GQA4
+#define FAL_FWD_VARLEN_GQA4 1   // varlen head_dim 128, Hq/Hkv a multiple of 4: the four-heads pipelined layout
+#endif
 size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t max_seqlen_q, int64_t head_dim) {
   (void)max_seqlen_q;
   // small problems: the kernel derives its work items itself
   if (num_seqs <= kVarlenSmallSeqs && total_q <= kVarlenSmallTokens) return 0;
-  const int bm = fwd_block_m_varlen(head_dim_ok(head_dim) ? (int)head_dim : 128);
+  // (head_dim 128 may run 64-row items: the four-heads layout, which the heads decide)
+  const int bm = head_dim == 128 && FAL_FWD_VARLEN_GQA4 ? 64 : fwd_block_m_varlen(head_dim_ok(head_dim) ? (int)head_dim : 128);
   const int64_t cap = (total_q + bm - 1) / bm + num_seqs;
   return align256((size_t)cap * sizeof(int2));
 }
@@ -255,7 +259,10 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
     return fail(FAL_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, workspace_bytes);
   if (num_seqs == 0 || total_q == 0) return ok();
 
-  const int bm = fwd_block_m_varlen((int)head_dim);
+  // head_dim 128 with Hq/Hkv a multiple of 4: the pipelined kernel's four-heads layout
+  // (64 rows of four query heads per workgroup) over the work list
+  const bool gqa4 = FAL_FWD_VARLEN_GQA4 && fwd_gqa4_ok((int)head_dim, heads_q, heads_kv);
+  const int bm = gqa4 ? 64 : fwd_block_m_varlen((int)head_dim);
   const int cap = (int)((total_q + bm - 1) / bm + num_seqs);
   hipStream_t st = static_cast<hipStream_t>(stream);
   int2* work = nullptr;
@@ -292,7 +299,8 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
   p.num_seqs = (int)num_seqs;
   p.n_qtiles = cap;   // work-list capacity (an upper bound on the item count)
   const int64_t groups8 = ((int64_t)cap * heads_kv + 7) / 8 * 8;
-  const int64_t nblocks = groups8 * (heads_q / heads_kv);
+  p.gqa4 = gqa4 ? 1 : 0;
+  const int64_t nblocks = groups8 * (heads_q / heads_kv / (gqa4 ? 4 : 1));
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
   return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), st),
                        "fal_fwd_varlen");

@@ -99,9 +99,11 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm
     // in work-list order (heaviest first), and the G heads of a group, which read the
     // same K/V, run back to back on one XCD (one L2).  The grid is padded to a multiple
     // of 8 groups; padding blocks exit.
+    // gqa4: one workgroup per four query heads of a group (wave w takes head 4*hg + w)
     const int g = p.Hq / p.Hkv;
+    const int ng = p.gqa4 ? g >> 2 : g;
     const int k8 = blockIdx.x >> 3;
-    const int grp = (k8 / g) * 8 + (blockIdx.x & 7);
+    const int grp = (k8 / ng) * 8 + (blockIdx.x & 7);
     const int item = grp / p.Hkv;
     if (item >= p.n_qtiles) return false;
     int seq, qt;
@@ -113,7 +115,8 @@ __device__ __forceinline__ bool fwd_item(const FwdParams& p, FwdItem& it, int bm
     } else if (!varlen_item_small(p.cu_q, p.num_seqs, p.total_q, bm, item, seq, qt)) {
       return false;
     }
-    it.hq = (grp % p.Hkv) * g + k8 % g;
+    it.hq = __builtin_amdgcn_readfirstlane((grp % p.Hkv) * g +
+                                           (p.gqa4 ? (k8 % ng) * 4 + (int)(threadIdx.x >> 6) : k8 % ng));
     it.b = 0;
     it.split = 0;
     it.qt = qt;
@@ -802,7 +805,7 @@ fwd_kernel(FwdParams p) {
     return;
   }
   // ---- resolve this workgroup's (batch/sequence, head, query tile) ----
-  if (!fwd_item<CAUSAL>(p, it, NW * 32 * RB)) return;
+  if (!fwd_item<CAUSAL>(p, it, p.gqa4 ? 64 : NW * 32 * RB)) return;
   vec8<T> qio[RB][D / 16];
   fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, it, false, qio);
 }
@@ -1012,7 +1015,9 @@ static hipError_t launch_fwd_t(const FwdParams& p, int causal, dim3 grid, hipStr
 }
 template <int D>
 static hipError_t launch_fwd_d(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
-  if (p.cu_q)
+  // packed sequences keep their own tile configuration, except under the four-heads
+  // layout, which runs the batched (pipelined) kernel over the work list
+  if (p.cu_q && !p.gqa4)
     return p.bf16 ? launch_fwd_t<bf16_t, D, true>(p, causal, grid, st)
                   : launch_fwd_t<half_t, D, true>(p, causal, grid, st);
   return p.bf16 ? launch_fwd_t<bf16_t, D, false>(p, causal, grid, st)
