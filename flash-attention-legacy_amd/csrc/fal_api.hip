@@ -230,6 +230,9 @@ size_t fal_fwd_varlen_workspace_size(int64_t num_seqs, int64_t total_q, int64_t 
 #ifndef FAL_BWD_DQ_VARLEN_ORDER
 #define FAL_BWD_DQ_VARLEN_ORDER 2
 #endif
+#ifndef FAL_FWD_VARLEN_PAIR
+#define FAL_FWD_VARLEN_PAIR 1   // four-heads varlen with a work list: pairs of query tiles per workgroup
+#endif
 #ifndef FAL_FWD_VARLEN_ORDER
 #define FAL_FWD_VARLEN_ORDER 2   // 2: grouped by sequence; 1: heaviest tile index first over all sequences
 #endif
@@ -264,6 +267,10 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
   const bool gqa4 = FAL_FWD_VARLEN_GQA4 && fwd_gqa4_ok((int)head_dim, heads_q, heads_kv);
   const int bm = gqa4 ? 64 : fwd_block_m_varlen((int)head_dim);
   const int cap = (int)((total_q + bm - 1) / bm + num_seqs);
+  // with a work list, the four-heads layout takes pairs of query tiles of a sequence
+  // (ceil(nt/2) list entries per sequence: at most half the tiles plus one each)
+  const bool vpair = gqa4 && FAL_FWD_VARLEN_PAIR && need > 0;
+  const int items = vpair ? (int)((total_q + bm - 1) / bm / 2 + num_seqs + 1) : cap;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int2* work = nullptr;
   if (need) {
@@ -273,7 +280,7 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
     int nb = cdiv((int)(max_seqlen_q > 0 ? max_seqlen_q : 1), bm);
     nb = nb < 1 ? 1 : (nb > 8192 ? 8192 : nb);
     hipError_t e = launch_varlen_schedule(cu_seqlens_q, (int)num_seqs, (int)total_q, bm, nb,
-                                          FAL_FWD_VARLEN_ORDER, work, cap, st);
+                                          vpair ? 4 : FAL_FWD_VARLEN_ORDER, work, cap, st);
     if (e != hipSuccess) return launch_status(e, "fal_fwd_varlen schedule");
   }
 
@@ -297,9 +304,10 @@ static int fal_fwd_varlen_impl(const void* q, const void* k, const void* v, void
   p.cu_k = cu_seqlens_k;
   p.work = work;
   p.num_seqs = (int)num_seqs;
-  p.n_qtiles = cap;   // work-list capacity (an upper bound on the item count)
-  const int64_t groups8 = ((int64_t)cap * heads_kv + 7) / 8 * 8;
+  p.n_qtiles = items;   // an upper bound on the list entries (the list holds `cap` slots)
+  const int64_t groups8 = ((int64_t)items * heads_kv + 7) / 8 * 8;
   p.gqa4 = gqa4 ? 1 : 0;
+  p.persist = vpair ? 1 : 0;   // each workgroup walks its pair's two items
   const int64_t nblocks = groups8 * (heads_q / heads_kv / (gqa4 ? 4 : 1));
   if (nblocks > 0x7fffffff) return fail(FAL_ERR_INVALID, "problem too large for one launch");
   return launch_status(launch_fwd(p, (int)head_dim, is_causal != 0, dim3((unsigned)nblocks), st),

@@ -777,7 +777,46 @@ __device__ __forceinline__ bool fwd_item_persist(const FwdParams& p, FwdItem& it
   return true;
 }
 
-template <class T, int D, int NW, int BN, bool CAUSAL, int RB>
+// Packed sequences under the four-heads layout with a work list of pairs (schedule
+// order 4): workgroup (pair, KV head, head quad) takes the pair's query tiles nt-1-j and
+// j of one sequence, heaviest first, through the same two-item walk as the persistent
+// grid (the second item's Q and first K/V tiles load during the first one's epilogue).
+// i = 0: the heavy tile; i = 1: the light one unless it is the same tile.
+template <bool CAUSAL>
+__device__ __forceinline__ bool fwd_item_vpair(const FwdParams& p, FwdItem& it, int i) {
+  if (i > 1) return false;
+  const int g = p.Hq / p.Hkv, ng = g >> 2;
+  const int k8 = blockIdx.x >> 3;
+  const int grp = (k8 / ng) * 8 + (blockIdx.x & 7);
+  const int item = grp / p.Hkv;
+  if (item >= p.n_qtiles) return false;
+  const int2 wk = p.work[item];
+  const int seq = __builtin_amdgcn_readfirstlane(wk.x), j = __builtin_amdgcn_readfirstlane(wk.y);
+  if (seq < 0) return false;
+  int qo, nq, ko, nk;
+  seg_bounds(p.cu_q, seq, p.total_q, qo, nq);
+  seg_bounds(p.cu_k, seq, p.total_k, ko, nk);
+  // (uniform values: the pipelined loop takes them as scalar operands)
+  it.q_off = __builtin_amdgcn_readfirstlane(qo);
+  it.nq = __builtin_amdgcn_readfirstlane(nq);
+  it.k_off = __builtin_amdgcn_readfirstlane(ko);
+  it.nk = __builtin_amdgcn_readfirstlane(nk);
+  const int nt = cdiv(it.nq, 64);
+  const int hi = nt - 1 - j, lo = j;
+  if (i == 1 && lo >= hi) return false;
+  it.qt = i == 0 ? hi : lo;
+  it.b = 0;
+  it.hq = __builtin_amdgcn_readfirstlane((grp % p.Hkv) * g + (k8 % ng) * 4 + (int)(threadIdx.x >> 6));
+  it.split = 0;
+  it.pre = 0;
+  it.qpre = 0;
+  return true;
+}
+
+// VPAIR: packed sequences, each workgroup walking the two items of one pair of the
+// work list (fwd_item_vpair); a separate instantiation, so the batched kernel keeps
+// its own register allocation.
+template <class T, int D, int NW, int BN, bool CAUSAL, int RB, bool VPAIR = false>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((RB == 2 && D >= 128) ? 1 : (D <= 128 ? FAL_FWD_WPE : 1), 8)))
 fwd_kernel(FwdParams p) {
@@ -793,9 +832,15 @@ fwd_kernel(FwdParams p) {
     // ends with a barrier after its O left LDS and may issue the next item's first copies
     FwdItem nx;
     vec8<T> qio[RB][D / 16];
-    bool have = fwd_item_persist<CAUSAL>(p, it, 0);
+    auto item = [&](FwdItem& x, int i) {
+      if constexpr (VPAIR)
+        return fwd_item_vpair<CAUSAL>(p, x, i);
+      else
+        return fwd_item_persist<CAUSAL>(p, x, i);
+    };
+    bool have = item(it, 0);
     for (int i = 0; have; ++i) {
-      const bool more = fwd_item_persist<CAUSAL>(p, nx, i + 1);
+      const bool more = item(nx, i + 1);
       const int r = fwd_body<T, D, NW, BN, CAUSAL, RB>(p, it, smem, nx, more, qio);
       nx.pre = r & 3;
       nx.qpre = r >> 2;
@@ -910,13 +955,14 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
   if (descending >= 2) {
     // Grouped by sequence: longest sequences first (bucketed by tile count), each
     // sequence's tiles contiguous; 2: last tile first (query-outer causal work grows
-    // with the tile index), 3: first tile first (KV-outer causal work shrinks with it).
+    // with the tile index), 3: first tile first (KV-outer causal work shrinks with it),
+    // 4: pairs (s, j) for j < ceil(nt/2), the tiles nt-1-j and j of one workgroup.
     // The workgroups an XCD runs at once then share one or two sequences' data in L2.
     for (int s = threadIdx.x; s < num_seqs; s += blockDim.x) {
       int off, len;
       seg_bounds(cu, s, rows, off, len);
       const int nt = cdiv(len, tile);
-      if (nt > 0) atomicAdd(&cnt[min(nt - 1, nbuckets - 1)], nt);
+      if (nt > 0) atomicAdd(&cnt[min(nt - 1, nbuckets - 1)], descending == 4 ? (nt + 1) / 2 : nt);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -934,8 +980,9 @@ varlen_schedule_kernel(const int* __restrict__ cu, int num_seqs, int rows, int t
       seg_bounds(cu, s, rows, off, len);
       const int nt = cdiv(len, tile);
       if (nt == 0) continue;
-      const int pos = atomicAdd(&cur[min(nt - 1, nbuckets - 1)], nt);
-      for (int t = 0; t < nt; ++t)
+      const int ne = descending == 4 ? (nt + 1) / 2 : nt;
+      const int pos = atomicAdd(&cur[min(nt - 1, nbuckets - 1)], ne);
+      for (int t = 0; t < ne; ++t)
         if (pos + t < capacity) work[pos + t] = make_int2(s, descending == 2 ? nt - 1 - t : t);
     }
     for (int i = total + threadIdx.x; i < capacity; i += blockDim.x) work[i] = make_int2(-1, -1);
@@ -1007,6 +1054,15 @@ struct FwdCfg {
 template <class T, int D, bool VARLEN>
 static hipError_t launch_fwd_t(const FwdParams& p, int causal, dim3 grid, hipStream_t st) {
   constexpr int NW = FwdCfg<D, VARLEN>::NW, BN = FwdCfg<D, VARLEN>::BN, RB = FwdCfg<D, VARLEN>::RB;
+  if constexpr (!VARLEN && D == 128 && RB == 2) {
+    if (p.cu_q && p.persist) {
+      if (causal)
+        hipLaunchKernelGGL((fwd_kernel<T, D, NW, BN, true, RB, true>), grid, dim3(NW * 64), 0, st, p);
+      else
+        hipLaunchKernelGGL((fwd_kernel<T, D, NW, BN, false, RB, true>), grid, dim3(NW * 64), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   if (causal)
     hipLaunchKernelGGL((fwd_kernel<T, D, NW, BN, true, RB>), grid, dim3(NW * 64), 0, st, p);
   else
