@@ -966,8 +966,16 @@ bwd_kv_pipe_kernel(BwdParams p) {
     {
       const char* wb = smem + ws * kKvOWave;
       const int cch = lane & 15;
-      T* dvb = (T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh;
-      T* dkb = (T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh;
+      // buffer resources over this wave's keys inside the sequence: stores past the end
+      // are dropped (no branch, no 64-bit address per store)
+      const int nkw = max(min(nk - kw0, 32), 0);
+      const __amdgpu_buffer_rsrc_t rs[2] = {
+          make_rsrc((T*)p.dv + (int64_t)b * p.dv_sb + (int64_t)hkv * p.dv_sh + (int64_t)kw0 * p.dv_ss,
+                    (uint32_t)((int64_t)nkw * p.dv_ss * 2)),
+          make_rsrc((T*)p.dk + (int64_t)b * p.dk_sb + (int64_t)hkv * p.dk_sh + (int64_t)kw0 * p.dk_ss,
+                    (uint32_t)((int64_t)nkw * p.dk_ss * 2))};
+      const int vo[2] = {((lane >> 4) * (int)p.dv_ss + cch * 8) * 2, ((lane >> 4) * (int)p.dk_ss + cch * 8) * 2};
+      const int rstep[2] = {(int)p.dv_ss * 8, (int)p.dk_ss * 8};   // 4 rows, in bytes
 #pragma unroll
       for (int which = 0; which < 2; ++which) {
         u32x4 x[8];
@@ -980,13 +988,7 @@ bwd_kv_pipe_kernel(BwdParams p) {
           x[jj] = nitems > 0 ? u32x4{lo.x, lo.y, hi.x, hi.y} : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int k = kw0 + jj * 4 + (lane >> 4);
-          if (k < nk) {
-            T* dst = which ? dkb + (int64_t)k * p.dk_ss : dvb + (int64_t)k * p.dv_ss;
-            st_u4(dst + cch * 8, x[jj]);
-          }
-        }
+        for (int jj = 0; jj < 8; ++jj) buffer_store16(rs[which], vo[which] + jj * rstep[which], x[jj]);
       }
     }
   }
@@ -1211,7 +1213,13 @@ bwd_dq_kernel(BwdParams p) {
       // each 16-byte store instruction covering 4 whole rows
       const char* wb = (const char*)smem + ws * kDqOWave;
       const int cch = lane & 15;
-      T* dqb = (T*)p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)q_off * p.dq_ss;
+      // a buffer resource over this wave's rows inside the sequence: stores past the end
+      // are dropped (no branch, no 64-bit address per store)
+      const int wr0 = m0 + ws * 32;
+      const __amdgpu_buffer_rsrc_t dqrs =
+          make_rsrc((T*)p.dq + (int64_t)b * p.dq_sb + (int64_t)hq * p.dq_sh + (int64_t)(q_off + wr0) * p.dq_ss,
+                    (uint32_t)((int64_t)max(min(nq - wr0, 32), 0) * p.dq_ss * 2));
+      const int dvo = ((lane >> 4) * (int)p.dq_ss + cch * 8) * 2;
       f32x4 a0[8], a1[8];
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
@@ -1224,14 +1232,13 @@ bwd_dq_kernel(BwdParams p) {
       }
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
-        const int grow = m0 + ws * 32 + jj * 4 + (lane >> 4);
         V8 h;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           h[e] = (T)(a0[jj][e] * p.scale);
           h[4 + e] = (T)(a1[jj][e] * p.scale);
         }
-        if (grow < nq) st_u4(dqb + (int64_t)grow * p.dq_ss + cch * 8, __builtin_bit_cast(u32x4, h));
+        buffer_store16(dqrs, dvo + jj * 4 * (int)p.dq_ss * 2, __builtin_bit_cast(u32x4, h));
       }
     }
     continue;

@@ -214,6 +214,12 @@ __device__ __forceinline__ void global_to_lds16(const void* src, void* lds_wave_
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
 }
+// 16-byte store through a raw buffer resource: a store whose offset is past the
+// resource's byte count is dropped, so rows past the end of a sequence need no branch.
+// The row goes in `voffset` (the range check covers it; an SGPR offset would not be).
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t rs, int voffset, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, voffset, 0, 0);
+}
 // 16-byte buffer -> LDS copy (buffer_load_dwordx4 ... lds); lane i writes bytes
 // [16 i, 16 i + 16) of `lds_wave_base` (uniform across the wave).
 // AUX: cache-policy bits of the load.

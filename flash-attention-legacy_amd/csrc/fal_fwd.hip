@@ -597,7 +597,14 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
           lbase[(int64_t)row[rb] * p.l_ss] = l_tot > 0.f ? (m_run[rb] + fast_log2(l_tot)) * kLn2 : -INFINITY;
       }
       const int cch = lane & 15;               // 16-byte chunk of the row
-      const int wr0 = m0 + (gqa4 ? 0 : w) * RB * 32;
+      const int wr0 = m0 + (gqa4 ? 0 : ws) * RB * 32;   // (ws: the wave index as a scalar)
+      // one buffer resource over this wave's rows inside the sequence: stores past its
+      // end are dropped, so a store needs no branch and no 64-bit address (at most 64
+      // rows of a sequence stride below 2^22 elements: offsets below 2^31)
+      const __amdgpu_buffer_rsrc_t ors =
+          make_rsrc(obase + (int64_t)wr0 * p.o_ss,
+                    (uint32_t)min((int64_t)max(min(nq - wr0, RB * 32), 0) * p.o_ss * 2, (int64_t)0x7fffffff));
+      const int ovo = ((lane >> 4) * (int)p.o_ss + cch * 8) * 2;
       // per 16 rows: all LDS reads and row factors first, then the stores (one wait, not
       // one per row)
 #pragma unroll
@@ -622,7 +629,7 @@ __device__ __forceinline__ int fwd_body(const FwdParams& p, const FwdItem& it, T
             h[e] = (T)(a0[jj][e] * iv[jj]);
             h[4 + e] = (T)(a1[jj][e] * iv[jj]);
           }
-          if (wr0 + r < nq) st_u4(obase + (int64_t)(wr0 + r) * p.o_ss + cch * 8, __builtin_bit_cast(u32x4, h));
+          buffer_store16(ors, ovo + (r - (lane >> 4)) * (int)p.o_ss * 2, __builtin_bit_cast(u32x4, h));
         }
       }
       stored = true;
