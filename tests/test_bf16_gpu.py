@@ -139,6 +139,30 @@ def test_varlen_forward_backward(causal):
         a += n
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_four_heads_pair_walk(causal):
+    """bf16 on the varlen pair walk (head dim 128, Hq/Hkv = 4, more than 64 sequences so
+    the schedule kernel builds the pair list): O and L of every sequence against the
+    oracle."""
+    from flash_attn_legacy import hip_ext
+    g = torch.Generator().manual_seed(95)
+    lens = [int(x) for x in torch.randint(1, 300, (68,), generator=g)] + [64, 65]
+    cu = cu_from_lens(lens)
+    tot, hq, hkv, d = sum(lens), 8, 2, 128
+    q, k, v = rbf((tot, hq, d), 96), rbf((tot, hkv, d), 97), rbf((tot, hkv, d), 98)
+    mx = max(lens)
+    o, lse = hip_ext.forward_varlen(q, k, v, cu, cu, mx, mx, 1.0 / math.sqrt(d), causal)
+    a = 0
+    for n in lens:
+        sl = slice(a, a + n)
+        t = lambda x: x[sl].transpose(0, 1).unsqueeze(0)
+        o_ref, l_ref = oracle_fwd(t(q), t(k), t(v), 1.0 / math.sqrt(d), causal)
+        check_out(t(o), o_ref)
+        err = (lse[sl].transpose(0, 1).unsqueeze(0).float().cpu() - l_ref.float()).abs().max().item()
+        assert err <= LSE_ATOL, err
+        a += n
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("layout", ["bshd", "bhsd"])
 def test_decode(d, layout):

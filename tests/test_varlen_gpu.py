@@ -145,6 +145,31 @@ def test_config_c4_forward():
             assert max_abs(o[c[i]:c[i + 1], hs], ref) <= FWD_ATOL, (i, g)
 
 
+def _list_lengths(n, lo, hi, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [int(x) for x in torch.randint(lo, hi + 1, (n,), generator=g)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (16, 2)])
+def test_four_heads_pair_walk(causal, hq, hkv):
+    """Head dim 128 with Hq/Hkv a multiple of 4 and a work list (more than 64 sequences):
+    each workgroup walks the query tiles nt-1-j and j of one sequence.  Lengths of 1,
+    63, 64, 65 and 129 rows give tile counts of 1 (a lone tile), odd and even; O and L
+    of every row against the float64 oracle."""
+    lens = _list_lengths(66, 1, 400, seed=90) + [1, 63, 64, 65, 129]
+    fwd_check(lens, lens, hq, hkv, 128, causal, seed=91)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_four_heads_pair_walk_unequal_segments(causal):
+    """The pair walk with query and key segments of different lengths (top-left causal
+    alignment within each sequence, empty query and key segments)."""
+    lq = _list_lengths(70, 0, 300, seed=92)
+    lk = [max(0, n + d) for n, d in zip(lq, _list_lengths(70, -40, 120, seed=93))]
+    fwd_check(lq, lk, 8, 2, 128, causal, seed=94)
+
+
 def test_config_c4_backward():
     """C4 lengths (16 sequences of U[64, 4096] tokens), 32/8 heads, d=128, causal: the
     native one-launch varlen backward against the per-sequence semantics of the
