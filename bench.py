@@ -362,7 +362,7 @@ def main():
                      "traffic": traffic,
                      "traffic_source": "profiles/fwd_c2_traffic.json: committed rocprofv3 --pmc FETCH_SIZE and "
                                        "WRITE_SIZE passes of this workload, not measured in this run",
-                     "kernel": "fwd_kernel<_Float16,128,4,64,true,2> (pipelined tile loop)",
+                     "kernel": "fwd_kernel<_Float16,128,4,64,true,2,false> (pipelined tile loop, persistent four-heads grid)",
                      "flops_per_launch": flops},
         "cpu_baseline": None if a.no_cpu else cpu_baseline(),
         "extra": extra,
