@@ -90,3 +90,24 @@ def test_graph_persistent_forward(hkv):
     scale = 1.0 / math.sqrt(d)
     o, lse = hip_ext.forward(q, k, v, scale, True)
     replay_check(lambda: hip_ext.forward(q, k, v, scale, True), (o, lse))
+
+
+def test_graph_varlen_pair_walk_and_backward():
+    """More than 64 packed sequences at head dim 128 with 8/2 heads: the schedule kernel
+    builds the pair list on the device, the four-heads forward walks it, and the
+    one-launch varlen backward builds its own lists; all captured and replayed."""
+    from flash_attn_legacy import hip_ext
+    g = torch.Generator().manual_seed(14)
+    lens = [int(x) for x in torch.randint(1, 300, (70,), generator=g)]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32, device="cuda")
+    tot, mx = sum(lens), max(lens)
+    q, k, v = randn((tot, 8, 128), seed=15), randn((tot, 2, 128), seed=16), randn((tot, 2, 128), seed=17)
+    do = randn((tot, 8, 128), seed=18)
+    scale = 1.0 / math.sqrt(128)
+    assert hip_ext._lib.fal_fwd_varlen_workspace_size(len(lens), tot, mx, 128) > 0   # the list path
+    o, lse = hip_ext.forward_varlen(q, k, v, cu, cu, mx, mx, scale, True)
+    grads = hip_ext.backward_varlen(do, q, k, v, o, lse, cu, cu, mx, mx, scale, True)
+    torch.cuda.synchronize()
+    replay_check(lambda: tuple(hip_ext.forward_varlen(q, k, v, cu, cu, mx, mx, scale, True)), (o, lse))
+    replay_check(lambda: tuple(hip_ext.backward_varlen(do, q, k, v, o, lse, cu, cu, mx, mx, scale, True)),
+                 tuple(grads))
